@@ -1,0 +1,191 @@
+// Element-wise parts of the MoE block: swiglu (activations.rs:55-59), the weighted combine with the
+// sigmoid-gated shared expert (moe.rs:84-93, 161-171), rms_norm / add_rms_norm around the block
+// (nuvec.rs:796-811), and a Linear's bias add (load.rs:302-305). All HBM-bound: 128-bit loads and
+// stores of 8 bf16 per thread, f32 inside, one bf16 rounding per reference op.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace mrun {
+
+__global__ __launch_bounds__(256) void swiglu_kernel(const bf16_t *__restrict__ g,
+                                                     const bf16_t *__restrict__ u, int64_t n,
+                                                     bf16_t *__restrict__ out) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+    if (i + 8 <= n) {
+        float gf[8], uf[8];
+        unpack8(*(const uint4 *)(g + i), gf);
+        unpack8(*(const uint4 *)(u + i), uf);
+        uint32_t o[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) o[k] = f2bf((gf[k] * sigmoidf_(gf[k])) * uf[k]);
+        *(uint4 *)(out + i) =
+            make_uint4(o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16),
+                       o[6] | (o[7] << 16));
+    } else {
+        for (int64_t k = i; k < n; ++k) {
+            const float gv = bf2f(g[k]);
+            out[k] = (bf16_t)f2bf((gv * sigmoidf_(gv)) * bf2f(u[k]));
+        }
+    }
+}
+
+hipError_t launch_swiglu(const bf16_t *g, const bf16_t *u, int64_t n, bf16_t *out,
+                         hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = (n + 256 * 8 - 1) / (256 * 8);
+    swiglu_kernel<<<dim3((unsigned)blocks), 256, 0, stream>>>(g, u, n, out);
+    return hipGetLastError();
+}
+
+// One workgroup per (token, 2048-column slab); thread = 8 columns.
+__global__ __launch_bounds__(256) void combine_kernel(const bf16_t *__restrict__ y,
+                                                      const uint32_t *__restrict__ inverse,
+                                                      const bf16_t *__restrict__ scores, int T,
+                                                      int k, int D, const bf16_t *__restrict__ sh_y,
+                                                      const bf16_t *__restrict__ sh_logit,
+                                                      bf16_t *__restrict__ out) {
+    const int t = blockIdx.x;
+    const int d = (blockIdx.y * 256 + threadIdx.x) * 8;
+    if (d >= D) return;
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+    for (int jj = 0; jj < k; ++jj) {
+        const int p = t * k + jj;
+        const size_t row = inverse ? inverse[p] : (uint32_t)p;
+        const float s = bf2f(scores[p]);
+        float yf[8];
+        unpack8(*(const uint4 *)(y + row * D + d), yf);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] += rbf(yf[i] * s);
+    }
+    uint32_t o[8];
+    if (sh_y) {
+        const float sg = rbf(sigmoidf_(bf2f(sh_logit[t])));
+        float sf[8];
+        unpack8(*(const uint4 *)(sh_y + (size_t)t * D + d), sf);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = f2bf(rbf(acc[i]) + rbf(sg * sf[i]));
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = f2bf(acc[i]);
+    }
+    *(uint4 *)(out + (size_t)t * D + d) = make_uint4(o[0] | (o[1] << 16), o[2] | (o[3] << 16),
+                                                     o[4] | (o[5] << 16), o[6] | (o[7] << 16));
+}
+
+hipError_t launch_combine(const bf16_t *y, const uint32_t *inverse, const bf16_t *scores, int T,
+                          int k, int D, const bf16_t *sh_y, const bf16_t *sh_logit, bf16_t *out,
+                          hipStream_t stream) {
+    dim3 grid(T, (D + 2047) / 2048);
+    combine_kernel<<<grid, 256, 0, stream>>>(y, inverse, scores, T, k, D, sh_y, sh_logit, out);
+    return hipGetLastError();
+}
+
+// One workgroup per row. With res: h = R(x + res) is written and normalised; else x is.
+__global__ __launch_bounds__(256) void rms_norm_kernel(const bf16_t *__restrict__ x,
+                                                       const bf16_t *__restrict__ res,
+                                                       const bf16_t *__restrict__ w, int D,
+                                                       float eps, bf16_t *h,
+                                                       bf16_t *__restrict__ y) {
+    const int r = blockIdx.x;
+    const bf16_t *xr = x + (size_t)r * D;
+    const bf16_t *rr = res ? res + (size_t)r * D : nullptr;
+    float ss = 0.f;
+    for (int d = threadIdx.x * 8; d < D; d += 2048) {
+        float xf[8];
+        unpack8(*(const uint4 *)(xr + d), xf);
+        if (rr) {
+            float rf[8];
+            unpack8(*(const uint4 *)(rr + d), rf);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xf[i] = rbf(xf[i] + rf[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss += xf[i] * xf[i];
+    }
+    __shared__ float red[4];
+    ss = group_sum<64>(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float tot = ((red[0] + red[1]) + red[2]) + red[3];
+    const float inv = 1.0f / sqrtf(tot / (float)D + eps);
+    for (int d = threadIdx.x * 8; d < D; d += 2048) {
+        float xf[8];
+        unpack8(*(const uint4 *)(xr + d), xf);
+        if (rr) {
+            float rf[8];
+            unpack8(*(const uint4 *)(rr + d), rf);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xf[i] = rbf(xf[i] + rf[i]);
+        }
+        uint32_t o[8], hv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float wv = w ? bf2f(w[d + i]) : 1.0f;
+            o[i] = f2bf(rbf(xf[i] * inv) * wv);
+            hv[i] = f2bf(xf[i]);
+        }
+        if (rr && h)
+            *(uint4 *)(h + (size_t)r * D + d) =
+                make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16),
+                           hv[6] | (hv[7] << 16));
+        *(uint4 *)(y + (size_t)r * D + d) = make_uint4(
+            o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16));
+    }
+}
+
+hipError_t launch_rms_norm(const bf16_t *x, const bf16_t *res, const bf16_t *w, int rows, int D,
+                           float eps, bf16_t *h, bf16_t *y, hipStream_t stream) {
+    rms_norm_kernel<<<rows, 256, 0, stream>>>(x, res, w, D, eps, h, y);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void add_bias_kernel(bf16_t *y, const bf16_t *__restrict__ b,
+                                                       int64_t total, int n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < total) y[i] = (bf16_t)f2bf(bf2f(y[i]) + bf2f(b[i % n]));
+}
+
+hipError_t launch_add_bias(bf16_t *y, const bf16_t *bias, int rows, int n, hipStream_t stream) {
+    const int64_t total = (int64_t)rows * n;
+    add_bias_kernel<<<dim3((unsigned)((total + 255) / 256)), 256, 0, stream>>>(y, bias, total, n);
+    return hipGetLastError();
+}
+
+// y[t][n] = R(x[t] . W[n]) (then R(. + bias[n])) for narrow outputs (a Linear with few rows, e.g.
+// the shared expert's gate): one wave per token, the rows of W in turn.
+__global__ __launch_bounds__(256) void rowdot_kernel(const bf16_t *__restrict__ x, int T, int D,
+                                                     const bf16_t *__restrict__ W, int N,
+                                                     const bf16_t *__restrict__ bias,
+                                                     bf16_t *__restrict__ y) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (t >= T) return;
+    const bf16_t *xr = x + (size_t)t * D;
+    for (int n = 0; n < N; ++n) {
+        const bf16_t *wr = W + (size_t)n * D;
+        float acc = 0.f;
+        for (int d = lane * 8; d < D; d += 512) {
+            float xf[8], wf[8];
+            unpack8(*(const uint4 *)(xr + d), xf);
+            unpack8(*(const uint4 *)(wr + d), wf);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc += xf[i] * wf[i];
+        }
+        acc = group_sum<64>(acc);
+        if (lane == 0) {
+            float v = rbf(acc);
+            if (bias) v = rbf(v + bf2f(bias[n]));
+            y[(size_t)t * N + n] = (bf16_t)f2bf(v);
+        }
+    }
+}
+
+hipError_t launch_rowdot(const bf16_t *x, int T, int D, const bf16_t *W, int N,
+                         const bf16_t *bias, bf16_t *y, hipStream_t stream) {
+    rowdot_kernel<<<dim3((T + 3) / 4), 256, 0, stream>>>(x, T, D, W, N, bias, y);
+    return hipGetLastError();
+}
+
+}  // namespace mrun

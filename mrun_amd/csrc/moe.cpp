@@ -1,0 +1,684 @@
+// Host layer of the MoE block: the C++ counterpart of the reference's operator surface and
+// layers, and the C ABI of include/mrun_moe.h over it.
+//
+//   mrun::tensor   — the facade ops the MoE path uses (crates/mrun-engine/src/tensor/nuvec.rs):
+//                    gather_qmm, quantized_matmul, linear, softmax/top-k (router), argsort-based
+//                    permute, swiglu, combine, rms_norm; each returns a Status carrying the
+//                    message, as the facade returns Result<_, Error(String)>.
+//   mrun::models   — SparseMoe::forward (models/moe.rs:149-174) composed from those ops, with the
+//                    decode (GEMV) or prefill (MFMA) schedule chosen from the token count.
+//
+// Nothing here allocates device memory: scratch comes from the caller's workspace.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+#include <string>
+
+#include "kernels.hpp"
+#include "mrun_moe.h"
+
+namespace mrun {
+
+// ---------------------------------------------------------------------------------------------
+// Status: the facade's Result<_, Error(String)>
+
+struct Status {
+    int code = MRUN_OK;
+    std::string msg;
+    bool ok() const { return code == MRUN_OK; }
+};
+
+static Status Ok() { return Status{}; }
+static Status Err(int code, std::string msg) { return Status{code, std::move(msg)}; }
+
+static thread_local std::string g_last_error;
+
+static int report(const Status &s) {
+    g_last_error = s.ok() ? std::string() : s.msg;
+    return s.code;
+}
+
+static Status hip_status(hipError_t e, const char *what) {
+    if (e == hipSuccess) return Ok();
+    return Err(MRUN_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define TRY(expr)                         \
+    do {                                  \
+        Status _s = (expr);               \
+        if (!_s.ok()) return _s;          \
+    } while (0)
+#define TRY_HIP(expr, what) TRY(hip_status((expr), (what)))
+
+static bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+static QW qw_of(const mrun_quantized &q) {
+    return QW{q.weight, q.scales, q.biases, q.experts, q.out, q.in, q.group_size, q.bits};
+}
+
+// ---------------------------------------------------------------------------------------------
+// validation: Quantized::new / QParams::checked / infer (nuvec.rs:609-626, load.rs:14-42, 131-156)
+
+static Status check_quantized(const mrun_quantized *q, const std::string &path, int experts,
+                              int out, int in) {
+    if (!q || !q->weight || !q->scales) return Err(MRUN_ERR_INVALID, path + ": missing tensors");
+    if (q->experts != experts || q->out != out || q->in != in)
+        return Err(MRUN_ERR_INVALID,
+                   path + ": shape [" + std::to_string(q->experts) + ", " +
+                       std::to_string(q->out) + ", " + std::to_string(q->in) + "], expected [" +
+                       std::to_string(experts) + ", " + std::to_string(out) + ", " +
+                       std::to_string(in) + "]");
+    const bool bits_ok = q->bits == 4 || q->bits == 8;
+    const bool group_ok = q->group_size == 32 || q->group_size == 64 || q->group_size == 128;
+    if (!bits_ok || !group_ok)
+        return Err(MRUN_ERR_INVALID, path + ": " + std::to_string(q->bits) +
+                                         " bits with group size " + std::to_string(q->group_size) +
+                                         " is not supported (affine 4 or 8 bits, groups of 32, "
+                                         "64 or 128)");
+    if (q->in % q->group_size != 0)
+        return Err(MRUN_ERR_INVALID, path + ": " + std::to_string(q->in / q->group_size) +
+                                         " scale groups do not divide the input width " +
+                                         std::to_string(q->in));
+    if (q->bits != 4)
+        return Err(MRUN_ERR_UNSUPPORTED,
+                   path + ": " + std::to_string(q->bits) + "-bit weights are not run by this build");
+    if (!aligned16(q->weight)) return Err(MRUN_ERR_INVALID, path + ": codes must be 16-byte aligned");
+    return Ok();
+}
+
+static Status check_ptr(const void *p, const char *what) {
+    if (!p) return Err(MRUN_ERR_INVALID, std::string(what) + " is null");
+    if (!aligned16(p)) return Err(MRUN_ERR_INVALID, std::string(what) + " must be 16-byte aligned");
+    return Ok();
+}
+
+static Status check_config(const mrun_moe_config &c) {
+    if (c.hidden <= 0 || c.experts <= 0 || c.intermediate <= 0)
+        return Err(MRUN_ERR_INVALID, "config: hidden, experts and intermediate must be positive");
+    if (c.top_k < 1 || c.top_k > c.experts)  // qwen3_5_moe.rs:508-513
+        return Err(MRUN_ERR_INVALID, "config: num_experts_per_tok " + std::to_string(c.top_k) +
+                                         " must be in 1..=" + std::to_string(c.experts));
+    if (c.shared_intermediate < 0) return Err(MRUN_ERR_INVALID, "config: shared width < 0");
+    if (c.experts > 512) return Err(MRUN_ERR_UNSUPPORTED, "config: more than 512 experts");
+    if (c.top_k > 16) return Err(MRUN_ERR_UNSUPPORTED, "config: top_k above 16");
+    if (c.hidden % 32 != 0 || c.intermediate % 32 != 0 || c.shared_intermediate % 32 != 0)
+        return Err(MRUN_ERR_UNSUPPORTED, "config: widths must be multiples of 32");
+    return Ok();
+}
+
+static Status check_block(const mrun_sparse_moe *m) {
+    if (!m) return Err(MRUN_ERR_INVALID, "moe is null");
+    const mrun_moe_config &c = m->cfg;
+    TRY(check_config(c));
+    const int D = c.hidden, E = c.experts, I = c.intermediate, S = c.shared_intermediate;
+    // router: dense bf16 [E, D] (+ bias [E])
+    if (!m->gate.weight)
+        return Err(MRUN_ERR_UNSUPPORTED, "gate: quantized routers are not run by this build");
+    if (m->gate.out != E || m->gate.in != D)
+        return Err(MRUN_ERR_INVALID, "gate: shape must be [experts, hidden]");
+    TRY(check_ptr(m->gate.weight, "gate.weight"));
+    TRY(check_quantized(&m->switch_gate_proj, "switch_mlp.gate_proj", E, I, D));
+    TRY(check_quantized(&m->switch_up_proj, "switch_mlp.up_proj", E, I, D));
+    TRY(check_quantized(&m->switch_down_proj, "switch_mlp.down_proj", E, D, I));
+    if (S > 0) {
+        const mrun_linear *mlp[3] = {&m->shared_gate_proj, &m->shared_up_proj,
+                                     &m->shared_down_proj};
+        const char *names[3] = {"shared_expert.gate_proj", "shared_expert.up_proj",
+                                "shared_expert.down_proj"};
+        for (int i = 0; i < 3; ++i) {
+            if (mlp[i]->weight)
+                return Err(MRUN_ERR_UNSUPPORTED,
+                           std::string(names[i]) + ": dense shared experts are not run by this build");
+            if (mlp[i]->bias)
+                return Err(MRUN_ERR_INVALID, std::string(names[i]) + ".bias is not supported");
+        }
+        TRY(check_quantized(&m->shared_gate_proj.q, names[0], 1, S, D));
+        TRY(check_quantized(&m->shared_up_proj.q, names[1], 1, S, D));
+        TRY(check_quantized(&m->shared_down_proj.q, names[2], 1, D, S));
+        if (!m->shared_expert_gate.weight)
+            return Err(MRUN_ERR_UNSUPPORTED,
+                       "shared_expert_gate: quantized gates are not run by this build");
+        if (m->shared_expert_gate.out != 1 || m->shared_expert_gate.in != D)
+            return Err(MRUN_ERR_INVALID, "shared_expert_gate: shape must be [1, hidden]");
+        TRY(check_ptr(m->shared_expert_gate.weight, "shared_expert_gate.weight"));
+    }
+    return Ok();
+}
+
+// ---------------------------------------------------------------------------------------------
+// workspace plan (the counterpart of SparseMoe::scratch_per_token, moe.rs:176-187)
+
+struct Plan {
+    size_t logits, ids, scores, offsets, order, inverse, token, active, n_active, tiles, n_tiles;
+    size_t act, y, sh_logit, sh_act, sh_y, total;
+    int max_tiles;
+};
+
+static size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static Plan make_plan(const mrun_moe_config &c, int T) {
+    Plan p{};
+    size_t at = 0;
+    auto take = [&](size_t bytes) {
+        size_t o = at;
+        at += a256(bytes);
+        return o;
+    };
+    const size_t E = c.experts, D = c.hidden, I = c.intermediate, S = c.shared_intermediate;
+    const size_t P = (size_t)T * c.top_k;
+    p.max_tiles = (int)((P + kGemmTileM - 1) / kGemmTileM + E);
+    p.logits = take(2 * (size_t)T * E);
+    p.ids = take(4 * P);
+    p.scores = take(2 * P);
+    p.offsets = take(4 * (E + 1));
+    p.order = take(4 * P);
+    p.inverse = take(4 * P);
+    p.token = take(4 * P);
+    p.active = take(4 * E);
+    p.n_active = take(4);
+    p.tiles = take(12 * (size_t)p.max_tiles);
+    p.n_tiles = take(4);
+    p.act = take(2 * P * I);
+    p.y = take(2 * P * D);
+    if (S > 0) {
+        p.sh_logit = take(2 * (size_t)T);
+        p.sh_act = take(2 * (size_t)T * S);
+        p.sh_y = take(2 * (size_t)T * D);
+    }
+    p.total = at;
+    return p;
+}
+
+namespace tensor {
+
+// ---------------------------------------------------------------------------------------------
+// facade ops
+
+// Linear::forward with a dense bf16 weight (load.rs:294-306): y = R(x W^T), then R(y + bias).
+static Status linear_dense(const bf16_t *x, int rows, const mrun_linear &l, bf16_t *y,
+                           hipStream_t s) {
+    const int N = l.out, K = l.in;
+    if (K % 8 != 0) return Err(MRUN_ERR_UNSUPPORTED, "linear: input width must be a multiple of 8");
+    if (rows > 16 && N < 16) {
+        TRY_HIP(launch_rowdot(x, rows, K, l.weight, N, l.bias, y, s), "linear (rowdot)");
+        return Ok();
+    }
+    if (rows > 16 && K % 64 == 0) {
+        GemmJob j{};
+        j.A = x, j.lda = K, j.a_div = 1, j.M = rows, j.N = N, j.K = K;
+        j.bd = l.weight, j.bias = l.bias, j.out = y, j.ldo = N;
+        TRY_HIP(launch_gemm(j, s), "linear (mfma)");
+        return Ok();
+    }
+    for (int r0 = 0; r0 < rows; r0 += 16) {
+        const int n = rows - r0 < 16 ? rows - r0 : 16;
+        TRY_HIP(launch_router_gemv(x + (size_t)r0 * K, n, K, l.weight, l.bias, N,
+                                   y + (size_t)r0 * N, nullptr, nullptr, s),
+                "linear (gemv)");
+    }
+    return Ok();
+}
+
+// quantized_matmul (nuvec.rs:660-663) over expert 0 of w: y [rows, w.out].
+static Status quantized_matmul(const bf16_t *x, int rows, const mrun_quantized &w, bf16_t *y,
+                               hipStream_t s) {
+    if (rows > 16 && w.in % 64 == 0) {
+        GemmJob j{};
+        j.A = x, j.lda = w.in, j.a_div = 1, j.M = rows, j.N = w.out, j.K = w.in;
+        j.w0 = qw_of(w), j.out = y, j.ldo = w.out;
+        TRY_HIP(launch_gemm(j, s), "quantized_matmul (mfma)");
+        return Ok();
+    }
+    GemvJob j{};
+    j.A = x, j.lda = w.in, j.a_div = 1, j.w0 = qw_of(w), j.max_slots = 1, j.rows = rows;
+    j.out = y, j.ldo = w.out;
+    TRY_HIP(launch_gemv(j, s), "quantized_matmul (gemv)");
+    return Ok();
+}
+
+static Status linear(const bf16_t *x, int rows, const mrun_linear &l, bf16_t *y, hipStream_t s) {
+    if (l.weight) return linear_dense(x, rows, l, y, s);
+    TRY(quantized_matmul(x, rows, l.q, y, s));
+    if (l.bias) TRY_HIP(launch_add_bias(y, l.bias, rows, l.out, s), "linear bias");
+    return Ok();
+}
+
+// Router: logits = gate(x); gates = softmax; ids = top-k; scores (moe.rs:151-159).
+static Status router(const mrun_sparse_moe &m, const bf16_t *x, int T, bf16_t *logits,
+                     bf16_t *gates, uint32_t *ids, bf16_t *scores, const PermuteOut *fused,
+                     hipStream_t s) {
+    const mrun_moe_config &c = m.cfg;
+    TRY(linear_dense(x, T, m.gate, logits, s));
+    TRY_HIP(launch_topk(logits, T, c.experts, c.top_k, c.norm_topk_prob != 0, gates, ids, scores,
+                        fused, s),
+            "router top-k");
+    return Ok();
+}
+
+}  // namespace tensor
+
+namespace models {
+
+// Benchmark instrumentation: an event recorded on the stream after each stage of the forward.
+struct Stages {
+    hipEvent_t *events = nullptr;
+    int n_events = 0;
+    int count = 0;
+    void mark(hipStream_t s) {
+        if (events && count + 1 < n_events) (void)hipEventRecord(events[count + 1], s);
+        ++count;
+    }
+};
+
+static const char *kDecodeStages = "router,topk_permute,gate_up,down_combine";
+static const char *kPrefillStages =
+    "router,shared_gate,topk,permute,gate_up,down,shared_gate_up,shared_down,combine";
+
+static bool is_decode(const mrun_moe_config &c, int T) {
+    const int I = c.intermediate, S = c.shared_intermediate;
+    // the fused down + combine kernel keeps T*k <= 128 pairs in LDS and needs rows of >= 256 codes
+    return T <= 16 && T * c.top_k <= 128 && I >= 256 && (S == 0 || S >= 256);
+}
+
+// ---------------------------------------------------------------------------------------------
+// SparseMoe::forward (moe.rs:149-174)
+
+static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int T, bf16_t *out,
+                                 char *ws, size_t ws_bytes, hipStream_t s, Stages *stg = nullptr) {
+    Stages none;
+    Stages &st = stg ? *stg : none;
+    if (st.events && st.n_events > 0) (void)hipEventRecord(st.events[0], s);
+    const mrun_moe_config &c = m.cfg;
+    const int D = c.hidden, E = c.experts, k = c.top_k, I = c.intermediate;
+    const int S = c.shared_intermediate;
+    const int P = T * k;
+    const Plan p = make_plan(c, T);
+    if (ws_bytes < p.total)
+        return Err(MRUN_ERR_WORKSPACE, "workspace of " + std::to_string(ws_bytes) +
+                                           " bytes, need " + std::to_string(p.total));
+    auto at = [&](size_t off) { return (void *)(ws + off); };
+    bf16_t *logits = (bf16_t *)at(p.logits);
+    uint32_t *ids = (uint32_t *)at(p.ids);
+    bf16_t *scores = (bf16_t *)at(p.scores);
+    PermuteOut po{};
+    po.offsets = (uint32_t *)at(p.offsets);
+    po.order = (uint32_t *)at(p.order);
+    po.inverse = (uint32_t *)at(p.inverse);
+    po.token = (uint32_t *)at(p.token);
+    po.active = (uint32_t *)at(p.active);
+    po.n_active = (uint32_t *)at(p.n_active);
+    po.tile_m = kGemmTileM;
+    Routing rt{po.offsets, po.active, po.n_active, (const uint32_t *)at(p.tiles),
+               (const uint32_t *)at(p.n_tiles)};
+    bf16_t *act = (bf16_t *)at(p.act);
+    bf16_t *y = (bf16_t *)at(p.y);
+    bf16_t *sh_logit = S ? (bf16_t *)at(p.sh_logit) : nullptr;
+    bf16_t *sh_act = S ? (bf16_t *)at(p.sh_act) : nullptr;
+    bf16_t *sh_y = S ? (bf16_t *)at(p.sh_y) : nullptr;
+    const int max_slots = E < P ? E : P;
+
+    const bool decode = is_decode(c, T);
+    const bool mfma = D % 64 == 0 && I % 64 == 0 && (S == 0 || S % 64 == 0);  // K of each product
+
+    if (decode) {
+        // 1. router logits (+ the shared expert's gate logit in the same launch)
+        TRY_HIP(launch_router_gemv(x, T, D, m.gate.weight, m.gate.bias, E, logits,
+                                   S ? m.shared_expert_gate.weight : nullptr, sh_logit, s),
+                "router");
+        if (S && m.shared_expert_gate.bias)
+            TRY_HIP(launch_add_bias(sh_logit, m.shared_expert_gate.bias, T, 1, s), "gate bias");
+        st.mark(s);
+        // 2. softmax, top-k, scores and the stable permute in one workgroup
+        TRY_HIP(launch_topk(logits, T, E, k, c.norm_topk_prob != 0, nullptr, ids, scores, &po, s),
+                "top-k");
+        st.mark(s);
+        // 3. gate/up + swiglu for every active expert, and the shared expert's gate/up
+        GemvJob g{};
+        g.A = x, g.lda = D, g.a_map = po.order, g.a_div = k;
+        g.w0 = qw_of(m.switch_gate_proj), g.w1 = qw_of(m.switch_up_proj);
+        g.routing = rt, g.has_routing = 1, g.max_slots = max_slots;
+        g.out = act, g.ldo = I, g.glu = 1;
+        if (S) {
+            g.xA = x, g.x_lda = D, g.xw0 = qw_of(m.shared_gate_proj.q);
+            g.xw1 = qw_of(m.shared_up_proj.q), g.x_rows = T, g.xout = sh_act, g.x_ldo = S;
+        }
+        TRY_HIP(launch_gemv(g, s), "gate/up");
+        st.mark(s);
+        // 4. down projection fused with the weighted combine and the gated shared expert
+        DownCombineJob dj{};
+        dj.act = act, dj.wd = qw_of(m.switch_down_proj), dj.routing = rt;
+        dj.max_slots = max_slots, dj.inverse = po.inverse, dj.scores = scores, dj.T = T, dj.k = k;
+        dj.has_shared = S > 0, dj.sh_act = sh_act;
+        if (S) dj.swd = qw_of(m.shared_down_proj.q);
+        dj.sh_logit = sh_logit, dj.out = out;
+        TRY_HIP(launch_down_combine(dj, s), "down/combine");
+        st.mark(s);
+        return Ok();
+    }
+
+    // prefill
+    TRY(tensor::linear_dense(x, T, m.gate, logits, s));
+    st.mark(s);
+    if (S) TRY(tensor::linear_dense(x, T, m.shared_expert_gate, sh_logit, s));
+    st.mark(s);
+    TRY_HIP(launch_topk(logits, T, E, k, c.norm_topk_prob != 0, nullptr, ids, scores, nullptr, s),
+            "top-k");
+    st.mark(s);
+    PermuteOut pt = po;
+    pt.tiles = (uint32_t *)at(p.tiles);
+    pt.n_tiles = (uint32_t *)at(p.n_tiles);
+    TRY_HIP(launch_permute(ids, P, k, E, pt, s), "permute");
+    st.mark(s);
+    if (mfma) {
+        GemmJob g{};
+        g.A = x, g.lda = D, g.a_map = po.order, g.a_div = k, g.N = I, g.K = D;
+        g.w0 = qw_of(m.switch_gate_proj), g.w1 = qw_of(m.switch_up_proj);
+        g.routing = rt, g.has_routing = 1, g.max_tiles = p.max_tiles;
+        g.out = act, g.ldo = I, g.glu = 1;
+        TRY_HIP(launch_gemm(g, s), "gate/up (mfma)");
+        st.mark(s);
+        GemmJob dn{};
+        dn.A = act, dn.lda = I, dn.a_div = 1, dn.N = D, dn.K = I;
+        dn.w0 = qw_of(m.switch_down_proj), dn.routing = rt, dn.has_routing = 1;
+        dn.max_tiles = p.max_tiles, dn.out = y, dn.ldo = D;
+        TRY_HIP(launch_gemm(dn, s), "down (mfma)");
+        st.mark(s);
+        if (S) {
+            GemmJob sg{};
+            sg.A = x, sg.lda = D, sg.a_div = 1, sg.M = T, sg.N = S, sg.K = D;
+            sg.w0 = qw_of(m.shared_gate_proj.q), sg.w1 = qw_of(m.shared_up_proj.q);
+            sg.out = sh_act, sg.ldo = S, sg.glu = 1;
+            TRY_HIP(launch_gemm(sg, s), "shared gate/up (mfma)");
+            st.mark(s);
+            GemmJob sd{};
+            sd.A = sh_act, sd.lda = S, sd.a_div = 1, sd.M = T, sd.N = D, sd.K = S;
+            sd.w0 = qw_of(m.shared_down_proj.q), sd.out = sh_y, sd.ldo = D;
+            TRY_HIP(launch_gemm(sd, s), "shared down (mfma)");
+            st.mark(s);
+        } else {
+            st.mark(s);
+            st.mark(s);
+        }
+    } else {
+        GemvJob g{};
+        g.A = x, g.lda = D, g.a_map = po.order, g.a_div = k;
+        g.w0 = qw_of(m.switch_gate_proj), g.w1 = qw_of(m.switch_up_proj);
+        g.routing = rt, g.has_routing = 1, g.max_slots = max_slots;
+        g.out = act, g.ldo = I, g.glu = 1;
+        if (S) {
+            g.xA = x, g.x_lda = D, g.xw0 = qw_of(m.shared_gate_proj.q);
+            g.xw1 = qw_of(m.shared_up_proj.q), g.x_rows = T, g.xout = sh_act, g.x_ldo = S;
+        }
+        TRY_HIP(launch_gemv(g, s), "gate/up (gemv)");
+        st.mark(s);
+        GemvJob dn{};
+        dn.A = act, dn.lda = I, dn.a_div = 1, dn.w0 = qw_of(m.switch_down_proj);
+        dn.routing = rt, dn.has_routing = 1, dn.max_slots = max_slots, dn.out = y, dn.ldo = D;
+        if (S) {
+            dn.xA = sh_act, dn.x_lda = S, dn.xw0 = qw_of(m.shared_down_proj.q);
+            dn.x_rows = T, dn.xout = sh_y, dn.x_ldo = D;
+        }
+        TRY_HIP(launch_gemv(dn, s), "down (gemv)");
+        st.mark(s);
+        st.mark(s);
+        st.mark(s);
+    }
+    TRY_HIP(launch_combine(y, po.inverse, scores, T, k, D, sh_y, sh_logit, out, s), "combine");
+    st.mark(s);
+    return Ok();
+}
+
+}  // namespace models
+}  // namespace mrun
+
+// ---------------------------------------------------------------------------------------------
+// C ABI
+
+using namespace mrun;
+
+extern "C" {
+
+const char *mrun_last_error(void) { return g_last_error.c_str(); }
+
+const char *mrun_version(void) { return "mrun-moe 0.1.0 (gfx950)"; }
+
+int mrun_moe_check(const mrun_sparse_moe *moe) { return report(check_block(moe)); }
+
+size_t mrun_moe_workspace_bytes(const mrun_moe_config *cfg, int32_t tokens) {
+    if (!cfg || tokens <= 0 || !check_config(*cfg).ok()) return 0;
+    return make_plan(*cfg, tokens).total;
+}
+
+int mrun_moe_forward(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t tokens,
+                     mrun_bf16 *out, void *workspace, size_t workspace_bytes,
+                     mrun_stream_t stream) {
+    Status st = check_block(moe);
+    if (st.ok() && tokens <= 0) st = Err(MRUN_ERR_INVALID, "tokens must be positive");
+    if (st.ok()) st = check_ptr(x, "x");
+    if (st.ok()) st = check_ptr(out, "out");
+    if (st.ok()) st = check_ptr(workspace, "workspace");
+    if (st.ok() && x == out) st = Err(MRUN_ERR_INVALID, "out must not alias x");
+    if (st.ok())
+        st = models::sparse_moe_forward(*moe, x, tokens, out, (char *)workspace, workspace_bytes,
+                                        (hipStream_t)stream);
+    return report(st);
+}
+
+int mrun_moe_forward_profiled(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t tokens,
+                              mrun_bf16 *out, void *workspace, size_t workspace_bytes,
+                              mrun_stream_t stream, void **events, int32_t n_events,
+                              int32_t *n_stages) {
+    Status st = check_block(moe);
+    if (st.ok() && tokens <= 0) st = Err(MRUN_ERR_INVALID, "tokens must be positive");
+    if (st.ok()) st = check_ptr(x, "x");
+    if (st.ok()) st = check_ptr(out, "out");
+    if (st.ok()) st = check_ptr(workspace, "workspace");
+    if (st.ok() && x == out) st = Err(MRUN_ERR_INVALID, "out must not alias x");
+    models::Stages stages;
+    stages.events = (hipEvent_t *)events;
+    stages.n_events = events ? n_events : 0;
+    if (st.ok())
+        st = models::sparse_moe_forward(*moe, x, tokens, out, (char *)workspace, workspace_bytes,
+                                        (hipStream_t)stream, &stages);
+    if (n_stages) *n_stages = stages.count;
+    return report(st);
+}
+
+const char *mrun_moe_stage_names(const mrun_moe_config *cfg, int32_t tokens) {
+    if (!cfg || tokens <= 0) return "";
+    return models::is_decode(*cfg, tokens) ? models::kDecodeStages : models::kPrefillStages;
+}
+
+int mrun_moe_router(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t tokens,
+                    mrun_bf16 *logits, mrun_bf16 *gates, uint32_t *ids, mrun_bf16 *scores,
+                    void *workspace, size_t workspace_bytes, mrun_stream_t stream) {
+    Status st = check_block(moe);
+    if (st.ok() && tokens <= 0) st = Err(MRUN_ERR_INVALID, "tokens must be positive");
+    if (st.ok()) st = check_ptr(x, "x");
+    if (st.ok() && (!ids || !scores)) st = Err(MRUN_ERR_INVALID, "ids and scores are required");
+    bf16_t *lg = logits;
+    if (st.ok() && !lg) {
+        const size_t need = 2 * (size_t)tokens * moe->cfg.experts;
+        if (!workspace || workspace_bytes < need)
+            st = Err(MRUN_ERR_WORKSPACE, "router needs " + std::to_string(need) +
+                                             " workspace bytes for the logits");
+        lg = (bf16_t *)workspace;
+    }
+    if (st.ok() && lg) st = check_ptr(lg, "logits");
+    if (st.ok())
+        st = tensor::router(*moe, x, tokens, lg, gates, ids, scores, nullptr, (hipStream_t)stream);
+    return report(st);
+}
+
+size_t mrun_moe_permute_workspace_bytes(int32_t pairs, int32_t experts) {
+    (void)pairs;
+    (void)experts;
+    return 0;
+}
+
+int mrun_moe_permute(const uint32_t *ids, int32_t pairs, int32_t top_k, int32_t experts,
+                     uint32_t *offsets, uint32_t *order, uint32_t *inverse, uint32_t *token,
+                     void *workspace, size_t workspace_bytes, mrun_stream_t stream) {
+    (void)workspace;
+    (void)workspace_bytes;
+    Status st;
+    if (!ids || !offsets) st = Err(MRUN_ERR_INVALID, "ids and offsets are required");
+    else if (pairs <= 0 || top_k <= 0 || pairs % top_k != 0)
+        st = Err(MRUN_ERR_INVALID, "pairs must be a positive multiple of top_k");
+    else if (experts <= 0 || experts > 1024)
+        st = Err(MRUN_ERR_UNSUPPORTED, "permute runs 1..=1024 experts");
+    if (st.ok()) {
+        PermuteOut po{};
+        po.offsets = offsets, po.order = order, po.inverse = inverse, po.token = token;
+        st = hip_status(launch_permute(ids, pairs, top_k, experts, po, (hipStream_t)stream),
+                        "permute");
+    }
+    return report(st);
+}
+
+size_t mrun_gather_qmm_workspace_bytes(int32_t n, int32_t experts) {
+    if (n <= 0 || experts <= 0) return 0;
+    const size_t max_tiles = (size_t)(n + kGemmTileM - 1) / kGemmTileM + experts;
+    return a256(4 * ((size_t)experts + 1)) + a256(4 * (size_t)n) + a256(4 * (size_t)experts) +
+           a256(4) + a256(12 * max_tiles) + a256(4);
+}
+
+int mrun_gather_qmm(const mrun_bf16 *x, int32_t x_rows, const mrun_quantized *w,
+                    const uint32_t *indices, int32_t n, int32_t sorted_indices, mrun_bf16 *out,
+                    void *workspace, size_t workspace_bytes, mrun_stream_t stream) {
+    (void)sorted_indices;  // the permute below orders any index list; sorted input stays put
+    Status st;
+    if (!w || !indices || x_rows <= 0 || n <= 0 || n % x_rows != 0)
+        st = Err(MRUN_ERR_INVALID, "gather_qmm: n must be a positive multiple of x_rows");
+    if (st.ok()) st = check_quantized(w, "gather_qmm weight", w->experts, w->out, w->in);
+    if (st.ok()) st = check_ptr(x, "x");
+    if (st.ok()) st = check_ptr(out, "out");
+    if (st.ok() && w->experts > 1024) st = Err(MRUN_ERR_UNSUPPORTED, "more than 1024 experts");
+    const size_t need = mrun_gather_qmm_workspace_bytes(n, w ? w->experts : 1);
+    if (st.ok() && (!workspace || workspace_bytes < need))
+        st = Err(MRUN_ERR_WORKSPACE, "gather_qmm needs " + std::to_string(need) + " bytes");
+    if (st.ok()) {
+        hipStream_t s = (hipStream_t)stream;
+        char *ws = (char *)workspace;
+        const int E = w->experts;
+        const size_t max_tiles = (size_t)(n + kGemmTileM - 1) / kGemmTileM + E;
+        PermuteOut po{};
+        size_t at = 0;
+        po.offsets = (uint32_t *)(ws + at), at += a256(4 * ((size_t)E + 1));
+        po.order = (uint32_t *)(ws + at), at += a256(4 * (size_t)n);
+        po.active = (uint32_t *)(ws + at), at += a256(4 * (size_t)E);
+        po.n_active = (uint32_t *)(ws + at), at += a256(4);
+        po.tiles = (uint32_t *)(ws + at), at += a256(12 * max_tiles);
+        po.n_tiles = (uint32_t *)(ws + at);
+        po.tile_m = kGemmTileM;
+        st = hip_status(launch_permute(indices, n, 1, E, po, s), "gather_qmm permute");
+        Routing rt{po.offsets, po.active, po.n_active, po.tiles, po.n_tiles};
+        const int per_x = n / x_rows;
+        if (st.ok() && n > 16 && w->in % 64 == 0) {
+            GemmJob j{};
+            j.A = x, j.lda = w->in, j.a_map = po.order, j.a_div = per_x, j.N = w->out, j.K = w->in;
+            j.w0 = qw_of(*w), j.routing = rt, j.has_routing = 1, j.max_tiles = (int)max_tiles;
+            j.o_map = po.order, j.out = out, j.ldo = w->out;
+            st = hip_status(launch_gemm(j, s), "gather_qmm (mfma)");
+        } else if (st.ok()) {
+            GemvJob j{};
+            j.A = x, j.lda = w->in, j.a_map = po.order, j.a_div = per_x, j.w0 = qw_of(*w);
+            j.routing = rt, j.has_routing = 1, j.max_slots = E < n ? E : n;
+            j.o_map = po.order, j.out = out, j.ldo = w->out;
+            st = hip_status(launch_gemv(j, s), "gather_qmm (gemv)");
+        }
+    }
+    return report(st);
+}
+
+int mrun_quantized_matmul(const mrun_bf16 *x, int32_t rows, const mrun_quantized *w,
+                          mrun_bf16 *out, mrun_stream_t stream) {
+    Status st;
+    if (!w || rows <= 0) st = Err(MRUN_ERR_INVALID, "quantized_matmul: bad arguments");
+    if (st.ok()) st = check_quantized(w, "quantized_matmul weight", 1, w->out, w->in);
+    if (st.ok()) st = check_ptr(x, "x");
+    if (st.ok()) st = check_ptr(out, "out");
+    if (st.ok()) st = tensor::quantized_matmul(x, rows, *w, out, (hipStream_t)stream);
+    return report(st);
+}
+
+int mrun_linear_forward(const mrun_linear *l, const mrun_bf16 *x, int32_t rows, mrun_bf16 *out,
+                        mrun_stream_t stream) {
+    Status st;
+    if (!l || rows <= 0) st = Err(MRUN_ERR_INVALID, "linear: bad arguments");
+    if (st.ok() && l->weight) st = check_ptr(l->weight, "weight");
+    if (st.ok() && !l->weight) st = check_quantized(&l->q, "linear weight", 1, l->out, l->in);
+    if (st.ok() && l->weight && (l->out <= 0 || l->in <= 0))
+        st = Err(MRUN_ERR_INVALID, "linear: bad shape");
+    if (st.ok()) st = check_ptr(x, "x");
+    if (st.ok()) st = check_ptr(out, "out");
+    if (st.ok()) st = tensor::linear(x, rows, *l, out, (hipStream_t)stream);
+    return report(st);
+}
+
+int mrun_swiglu(const mrun_bf16 *gate, const mrun_bf16 *up, int64_t n, mrun_bf16 *out,
+                mrun_stream_t stream) {
+    Status st;
+    if (n < 0) st = Err(MRUN_ERR_INVALID, "swiglu: n < 0");
+    if (st.ok()) st = check_ptr(gate, "gate");
+    if (st.ok()) st = check_ptr(up, "up");
+    if (st.ok()) st = check_ptr(out, "out");
+    if (st.ok()) st = hip_status(launch_swiglu(gate, up, n, out, (hipStream_t)stream), "swiglu");
+    return report(st);
+}
+
+int mrun_moe_combine(const mrun_bf16 *y, const uint32_t *inverse, const mrun_bf16 *scores,
+                     int32_t tokens, int32_t top_k, int32_t hidden, const mrun_bf16 *shared_y,
+                     const mrun_bf16 *shared_logit, mrun_bf16 *out, mrun_stream_t stream) {
+    Status st;
+    if (tokens <= 0 || top_k <= 0 || hidden <= 0 || hidden % 8 != 0)
+        st = Err(MRUN_ERR_INVALID, "combine: bad shape (hidden must be a multiple of 8)");
+    if (st.ok()) st = check_ptr(y, "y");
+    if (st.ok() && !scores) st = Err(MRUN_ERR_INVALID, "scores is null");
+    if (st.ok() && shared_y) st = check_ptr(shared_y, "shared_y");
+    if (st.ok() && shared_y && !shared_logit)
+        st = Err(MRUN_ERR_INVALID, "shared_y needs shared_logit");
+    if (st.ok()) st = check_ptr(out, "out");
+    if (st.ok())
+        st = hip_status(launch_combine(y, inverse, scores, tokens, top_k, hidden, shared_y,
+                                       shared_logit, out, (hipStream_t)stream),
+                        "combine");
+    return report(st);
+}
+
+int mrun_rms_norm(const mrun_bf16 *x, const mrun_bf16 *w, int32_t rows, int32_t hidden, float eps,
+                  mrun_bf16 *out, mrun_stream_t stream) {
+    Status st;
+    if (rows <= 0 || hidden <= 0 || hidden % 8 != 0)
+        st = Err(MRUN_ERR_INVALID, "rms_norm: bad shape (hidden must be a multiple of 8)");
+    if (st.ok()) st = check_ptr(x, "x");
+    if (st.ok()) st = check_ptr(out, "out");
+    if (st.ok() && x == out) st = Err(MRUN_ERR_INVALID, "rms_norm: out must not alias x");
+    if (st.ok())
+        st = hip_status(launch_rms_norm(x, nullptr, w, rows, hidden, eps, nullptr, out,
+                                        (hipStream_t)stream),
+                        "rms_norm");
+    return report(st);
+}
+
+int mrun_add_rms_norm(const mrun_bf16 *x, const mrun_bf16 *residual, const mrun_bf16 *w,
+                      int32_t rows, int32_t hidden, float eps, mrun_bf16 *h, mrun_bf16 *y,
+                      mrun_stream_t stream) {
+    Status st;
+    if (rows <= 0 || hidden <= 0 || hidden % 8 != 0)
+        st = Err(MRUN_ERR_INVALID, "add_rms_norm: bad shape (hidden must be a multiple of 8)");
+    if (st.ok()) st = check_ptr(x, "x");
+    if (st.ok()) st = check_ptr(residual, "residual");
+    if (st.ok()) st = check_ptr(h, "h");
+    if (st.ok()) st = check_ptr(y, "y");
+    if (st.ok() && (y == x || y == residual || y == h))
+        st = Err(MRUN_ERR_INVALID, "add_rms_norm: y must not alias its inputs");
+    if (st.ok())
+        st = hip_status(launch_rms_norm(x, residual, w, rows, hidden, eps, h, y,
+                                        (hipStream_t)stream),
+                        "add_rms_norm");
+    return report(st);
+}
+
+}  // extern "C"

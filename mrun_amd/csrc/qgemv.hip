@@ -1,0 +1,350 @@
+// Decode-shaped gathered 4-bit products (gather_qmm at T <= 16, nuvec.rs:670-686) and the fused
+// down projection + combine of the MoE block (moe.rs:79-93, 161-171).
+//
+// Layout: a weight row of K codes is K/8 u32 words; LPR lanes share a row, each lane owning
+// 32-code chunks (one 128-bit load) li, li+LPR, ...; a 32-code chunk always lies in one quant
+// group (32 | group). Per (row, pair) a lane computes scale*sum(x*q) + bias*sum(x) over its chunks
+// in f32, then the LPR lanes are summed by a fixed butterfly: the order depends on K only, never
+// on how many rows or pairs are in flight (rows of a batch keep their one-row bits).
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace mrun {
+
+// Rows of one pair chunk per extra (shared-expert) slot.
+constexpr int kExtraRowsPerSlot = 4;
+
+struct Chunk {
+    uint4 q;
+    float s, b;
+};
+
+// Keeps the packed codes opaque inside a loop, so the compiler does not hoist their conversion
+// to f32 (8x the registers) out of the per-pair loop.
+__device__ __forceinline__ void opaque(uint4 &q) {
+    asm volatile("" : "+v"(q.x), "+v"(q.y), "+v"(q.z), "+v"(q.w));
+}
+
+// sum_i x[i] * q[i] over 32 codes of a chunk; xs = sum of the 32 x values.
+__device__ __forceinline__ float dot32(const uint4 &q, const uint4 *xv) {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    float acc = 0.f;
+#pragma unroll
+    for (int wi = 0; wi < 4; ++wi) {
+        const uint32_t lo = w[wi] & 0x0f0f0f0fu, hi = (w[wi] >> 4) & 0x0f0f0f0fu;
+        const uint4 xx = xv[wi];
+        // codes 8wi..8wi+7 pair with x bf16 values 8wi..8wi+7 (xx.x holds x0,x1; ...)
+        acc += bf_lo(xx.x) * (float)(lo & 0xffu);
+        acc += bf_hi(xx.x) * (float)(hi & 0xffu);
+        acc += bf_lo(xx.y) * (float)((lo >> 8) & 0xffu);
+        acc += bf_hi(xx.y) * (float)((hi >> 8) & 0xffu);
+        acc += bf_lo(xx.z) * (float)((lo >> 16) & 0xffu);
+        acc += bf_hi(xx.z) * (float)((hi >> 16) & 0xffu);
+        acc += bf_lo(xx.w) * (float)(lo >> 24);
+        acc += bf_hi(xx.w) * (float)(hi >> 24);
+    }
+    return acc;
+}
+
+__device__ __forceinline__ float sum32(const uint4 *xv) {
+    float s = 0.f;
+#pragma unroll
+    for (int wi = 0; wi < 4; ++wi) {
+        s += bf_lo(xv[wi].x) + bf_hi(xv[wi].x);
+        s += bf_lo(xv[wi].y) + bf_hi(xv[wi].y);
+        s += bf_lo(xv[wi].z) + bf_hi(xv[wi].z);
+        s += bf_lo(xv[wi].w) + bf_hi(xv[wi].w);
+    }
+    return s;
+}
+
+__device__ __forceinline__ Chunk load_chunk(const QW &w, int e, int row, int ch) {
+    Chunk c;
+    const size_t r = (size_t)e * w.out + row;
+    const int words = w.in >> 3, groups = w.in / w.group;
+    c.q = *(const uint4 *)(w.codes + r * words + (size_t)ch * 4);
+    const int g = (ch * 32) / w.group;
+    c.s = bf2f(w.scales[r * groups + g]);
+    c.b = w.biases ? bf2f(w.biases[r * groups + g]) : 0.f;
+    return c;
+}
+
+// ---------------------------------------------------------------------------------------------
+
+template <bool GLU, int LPR, int CPL, int RG, int PCH>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvJob j) {
+    constexpr int RPI = 64 / LPR;      // rows per load instruction
+    constexpr int ROWS_W = RG * RPI;   // rows per wave
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int li = lane % LPR, rsub = lane / LPR;
+    const int slot = blockIdx.y;
+
+    const bf16_t *A;
+    int lda, a_div, e, lo, hi, ldo;
+    const uint32_t *a_map, *o_map;
+    QW w0, w1;
+    bf16_t *out;
+    if (slot < j.max_slots) {
+        if (j.has_routing) {
+            if ((uint32_t)slot >= *j.routing.n_active) return;
+            e = (int)j.routing.active[slot];
+            lo = (int)j.routing.offsets[e];
+            hi = (int)j.routing.offsets[e + 1];
+        } else {
+            if (slot > 0) return;
+            e = 0;
+            lo = 0;
+            hi = j.rows;
+        }
+        A = j.A, lda = j.lda, a_map = j.a_map, a_div = j.a_div;
+        w0 = j.w0, w1 = j.w1, o_map = j.o_map, out = j.out, ldo = j.ldo;
+    } else {
+        const int xs = slot - j.max_slots;
+        lo = xs * kExtraRowsPerSlot;
+        hi = min(j.x_rows, lo + kExtraRowsPerSlot);
+        if (lo >= hi) return;
+        e = 0;
+        A = j.xA, lda = j.x_lda, a_map = nullptr, a_div = 1;
+        w0 = j.xw0, w1 = j.xw1, o_map = nullptr, out = j.xout, ldo = j.x_ldo;
+    }
+    const int n_ch = w0.in >> 5;
+    const int row_base = (blockIdx.x * 4 + wave) * ROWS_W;
+
+    Chunk c0[RG][CPL], c1[RG][CPL];
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+        const int row = row_base + g * RPI + rsub;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int ch = li + c * LPR;
+            if (row < w0.out && ch < n_ch) {
+                c0[g][c] = load_chunk(w0, e, row, ch);
+                if (GLU) c1[g][c] = load_chunk(w1, e, row, ch);
+            } else {
+                c0[g][c] = Chunk{make_uint4(0, 0, 0, 0), 0.f, 0.f};
+                c1[g][c] = c0[g][c];
+            }
+        }
+    }
+
+    for (int p0 = lo; p0 < hi; p0 += PCH) {
+        uint4 xv[PCH][CPL][4];
+        float xs[PCH][CPL];
+#pragma unroll
+        for (int pp = 0; pp < PCH; ++pp) {
+            const int pos = p0 + pp;
+            const int arow = pos < hi ? (a_map ? (int)(a_map[pos] / (uint32_t)a_div) : pos) : -1;
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                const int ch = li + c * LPR;
+                if (arow >= 0 && ch < n_ch) {
+                    const uint4 *src = (const uint4 *)(A + (size_t)arow * lda + ch * 32);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) xv[pp][c][q] = src[q];
+                    xs[pp][c] = sum32(xv[pp][c]);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) xv[pp][c][q] = make_uint4(0, 0, 0, 0);
+                    xs[pp][c] = 0.f;
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < RG; ++g) {
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                opaque(c0[g][c].q);
+                if (GLU) opaque(c1[g][c].q);
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < RG; ++g) {
+            const int row = row_base + g * RPI + rsub;
+#pragma unroll
+            for (int pp = 0; pp < PCH; ++pp) {
+                float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    a0 += c0[g][c].s * dot32(c0[g][c].q, xv[pp][c]) + c0[g][c].b * xs[pp][c];
+                    if (GLU)
+                        a1 += c1[g][c].s * dot32(c1[g][c].q, xv[pp][c]) + c1[g][c].b * xs[pp][c];
+                }
+                a0 = group_sum<LPR>(a0);
+                if (GLU) a1 = group_sum<LPR>(a1);
+                const int pos = p0 + pp;
+                if (li == 0 && row < w0.out && pos < hi) {
+                    const int orow = o_map ? (int)o_map[pos] : pos;
+                    float v;
+                    if (GLU) {
+                        const float gt = rbf(a0), up = rbf(a1);
+                        v = (gt * sigmoidf_(gt)) * up;
+                    } else {
+                        v = a0;
+                    }
+                    out[(size_t)orow * ldo + row] = (bf16_t)f2bf(v);
+                }
+            }
+        }
+    }
+}
+
+template <bool GLU, int LPR, int CPL>
+static void launch_gemv_t(const GemvJob &j, hipStream_t stream) {
+    constexpr int RG = GLU ? 4 : 8;
+    constexpr int RPI = 64 / LPR;
+    constexpr int ROWS_B = 4 * RG * RPI;
+    const int extra = j.x_rows > 0 ? (j.x_rows + kExtraRowsPerSlot - 1) / kExtraRowsPerSlot : 0;
+    const int rows = (extra && j.xw0.out > j.w0.out) ? j.xw0.out : j.w0.out;
+    dim3 grid((rows + ROWS_B - 1) / ROWS_B, j.max_slots + extra);
+    gemv_kernel<GLU, LPR, CPL, RG, 1><<<grid, 256, 0, stream>>>(j);
+}
+
+template <bool GLU>
+static hipError_t launch_gemv_glu(const GemvJob &j, hipStream_t stream) {
+    const int n_ch = j.w0.in >> 5;
+    if (n_ch >= 64) {
+        const int cpl = (n_ch + 63) / 64;
+        if (cpl == 1) launch_gemv_t<GLU, 64, 1>(j, stream);
+        else if (cpl == 2) launch_gemv_t<GLU, 64, 2>(j, stream);
+        else if (cpl == 3) launch_gemv_t<GLU, 64, 3>(j, stream);
+        else if (cpl == 4) launch_gemv_t<GLU, 64, 4>(j, stream);
+        else return hipErrorInvalidValue;
+    } else if (n_ch >= 32) {
+        launch_gemv_t<GLU, 32, 2>(j, stream);
+    } else if (n_ch >= 16) {
+        launch_gemv_t<GLU, 16, 2>(j, stream);
+    } else if (n_ch >= 8) {
+        launch_gemv_t<GLU, 8, 2>(j, stream);
+    } else if (n_ch >= 4) {
+        launch_gemv_t<GLU, 4, 2>(j, stream);
+    } else if (n_ch >= 2) {
+        launch_gemv_t<GLU, 2, 2>(j, stream);
+    } else {
+        launch_gemv_t<GLU, 1, 1>(j, stream);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv(const GemvJob &j, hipStream_t stream) {
+    return j.glu ? launch_gemv_glu<true>(j, stream) : launch_gemv_glu<false>(j, stream);
+}
+
+// ---------------------------------------------------------------------------------------------
+// down projection + combine (decode)
+
+constexpr int kDownRows = 8;        // output rows (of D) per workgroup
+constexpr int kMaxPairs = 128;      // T*k
+constexpr int kMaxTokens = 16;
+
+template <int LPR, int CPL>
+__device__ __forceinline__ void down_rows(const QW &w, int e, const bf16_t *act, int lda,
+                                          int lo, int hi, int d0, int g, float (*yv)[kDownRows],
+                                          int li, int rsub) {
+    constexpr int RPI = 64 / LPR;
+    const int n_ch = w.in >> 5;
+    const int row = d0 + g * RPI + rsub;
+    Chunk c[CPL];
+#pragma unroll
+    for (int cc = 0; cc < CPL; ++cc) {
+        const int ch = li + cc * LPR;
+        if (ch < n_ch) c[cc] = load_chunk(w, e, row, ch);
+        else c[cc] = Chunk{make_uint4(0, 0, 0, 0), 0.f, 0.f};
+    }
+    for (int pos = lo; pos < hi; ++pos) {
+        float a = 0.f;
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc) opaque(c[cc].q);
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc) {
+            const int ch = li + cc * LPR;
+            if (ch < n_ch) {
+                uint4 xv[4];
+                const uint4 *src = (const uint4 *)(act + (size_t)pos * lda + ch * 32);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) xv[q] = src[q];
+                a += c[cc].s * dot32(c[cc].q, xv) + c[cc].b * sum32(xv);
+            }
+        }
+        a = group_sum<LPR>(a);
+        if (li == 0) yv[pos][g * RPI + rsub] = rbf(a);
+    }
+}
+
+template <int LPR, int CPL, int SLPR, int SCPL>
+__global__ __launch_bounds__(256) void down_combine_kernel(DownCombineJob j) {
+    constexpr int RPI = 64 / LPR, NRG = kDownRows / RPI;
+    constexpr int SRPI = 64 / SLPR, SNRG = kDownRows / SRPI;
+    __shared__ float yv[kMaxPairs][kDownRows];
+    __shared__ float ysh[kMaxTokens][kDownRows];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int d0 = blockIdx.x * kDownRows;
+    const int na = (int)*j.routing.n_active;
+    const int n_items = na * NRG;
+    for (int it = wave; it < n_items; it += 4) {
+        const int slot = it / NRG, g = it % NRG;
+        const int e = (int)j.routing.active[slot];
+        down_rows<LPR, CPL>(j.wd, e, j.act, j.wd.in, (int)j.routing.offsets[e],
+                            (int)j.routing.offsets[e + 1], d0, g, yv, lane % LPR, lane / LPR);
+    }
+    if (j.has_shared) {
+        // the shared expert's rows go to the waves after the routed items, round robin
+        for (int it = (wave - n_items % 4 + 4) % 4; it < SNRG; it += 4)
+            down_rows<SLPR, SCPL>(j.swd, 0, j.sh_act, j.swd.in, 0, j.T, d0, it, ysh, lane % SLPR,
+                                  lane / SLPR);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < j.T * kDownRows; i += 256) {
+        const int t = i / kDownRows, dd = i % kDownRows;
+        float acc = 0.f;
+        for (int jj = 0; jj < j.k; ++jj) {
+            const int p = t * j.k + jj;
+            const int pos = (int)j.inverse[p];
+            acc += rbf(yv[pos][dd] * bf2f(j.scores[p]));
+        }
+        float r = rbf(acc);
+        if (j.has_shared) {
+            const float sg = rbf(sigmoidf_(bf2f(j.sh_logit[t])));
+            r = rbf(r + rbf(sg * ysh[t][dd]));
+        }
+        j.out[(size_t)t * j.wd.out + d0 + dd] = (bf16_t)f2bf(r);
+    }
+}
+
+template <int LPR, int CPL>
+static hipError_t launch_down_s(const DownCombineJob &j, hipStream_t stream) {
+    dim3 grid(j.wd.out / kDownRows);
+    const int sch = j.has_shared ? (j.swd.in >> 5) : 16;
+    if (sch == 16)
+        down_combine_kernel<LPR, CPL, 16, 1><<<grid, 256, 0, stream>>>(j);
+    else if (sch >= 64 && sch <= 64 * 4) {
+        const int c = (sch + 63) / 64;
+        if (c == 1) down_combine_kernel<LPR, CPL, 64, 1><<<grid, 256, 0, stream>>>(j);
+        else if (c == 2) down_combine_kernel<LPR, CPL, 64, 2><<<grid, 256, 0, stream>>>(j);
+        else if (c == 3) down_combine_kernel<LPR, CPL, 64, 3><<<grid, 256, 0, stream>>>(j);
+        else down_combine_kernel<LPR, CPL, 64, 4><<<grid, 256, 0, stream>>>(j);
+    } else if (sch >= 32) {
+        down_combine_kernel<LPR, CPL, 32, 2><<<grid, 256, 0, stream>>>(j);
+    } else if (sch >= 8) {
+        down_combine_kernel<LPR, CPL, 8, 2><<<grid, 256, 0, stream>>>(j);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_down_combine(const DownCombineJob &j, hipStream_t stream) {
+    const int n_ch = j.wd.in >> 5;
+    if (n_ch == 16) return launch_down_s<16, 1>(j, stream);
+    if (n_ch >= 64 && n_ch <= 256) {
+        const int c = (n_ch + 63) / 64;
+        if (c == 1) return launch_down_s<64, 1>(j, stream);
+        if (c == 2) return launch_down_s<64, 2>(j, stream);
+        if (c == 3) return launch_down_s<64, 3>(j, stream);
+        return launch_down_s<64, 4>(j, stream);
+    }
+    if (n_ch >= 32) return launch_down_s<32, 2>(j, stream);
+    if (n_ch >= 8) return launch_down_s<8, 2>(j, stream);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace mrun

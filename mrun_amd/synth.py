@@ -1,0 +1,217 @@
+"""Seeded synthetic MoE blocks and activations (the generator spec is in include/mrun_synth.h).
+
+The benchmark configurations give the synthetic tensors by distribution only; this module makes
+them concrete: 4-bit affine weights with group 64, codes uniform 0..15, scales |N(0,0.02)|/7.5,
+biases -8*scale, a bf16 N(0,0.02) router (optionally Zipf-biased) and shared-expert gate, bf16
+N(0,1) activations. Arrays are host numpy arrays; bf16 is carried as uint16 bits.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_double, c_float, c_int32, c_size_t, c_uint16, c_uint32, c_uint64
+from dataclasses import dataclass, field
+from pathlib import Path
+
+import numpy as np
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libmrun_synth.so"
+BASE_SEED = 0x6D72756E2D6D6F65  # "mrun-moe"
+
+# tensor ids of the generator's seed derivation
+X, ROUTER_W, ROUTER_BIAS = 0, 1, 2
+GATE_CODES, GATE_SCALES, UP_CODES, UP_SCALES, DOWN_CODES, DOWN_SCALES = 3, 4, 5, 6, 7, 8
+SH_GATE_CODES, SH_GATE_SCALES, SH_UP_CODES, SH_UP_SCALES = 9, 10, 11, 12
+SH_DOWN_CODES, SH_DOWN_SCALES, SH_EXPERT_GATE = 13, 14, 15
+
+
+@dataclass(frozen=True)
+class Shape:
+    """MoeConfig (moe.rs:97-107)."""
+
+    hidden: int
+    experts: int
+    top_k: int
+    intermediate: int
+    shared: int = 0
+    norm_topk: bool = True
+    group: int = 64
+
+    @property
+    def name(self) -> str:
+        return f"D{self.hidden}_E{self.experts}_k{self.top_k}_I{self.intermediate}_S{self.shared}"
+
+
+# Qwen3.6-35B-A3B-like and Qwen3-Coder-480B-A35B-like blocks.
+QWEN36 = Shape(hidden=2048, experts=256, top_k=8, intermediate=512, shared=512)
+CODER = Shape(hidden=6144, experts=160, top_k=8, intermediate=2560, shared=0)
+
+# configuration ids of the seed derivation (the benchmark's configs[0..4])
+CFG_PLUMBING, CFG_DECODE, CFG_PREFILL_ZIPF, CFG_STACK, CFG_CODER = 0, 1, 2, 3, 4
+
+
+@dataclass
+class QTensor:
+    """An affine 4-bit stacked weight: codes [E, out, in/8] u32, scales/biases [E, out, in/g]."""
+
+    codes: np.ndarray
+    scales: np.ndarray
+    biases: np.ndarray | None
+    experts: int
+    out: int
+    in_: int
+    group: int
+    bits: int = 4
+
+    @property
+    def nbytes(self) -> int:
+        b = self.codes.nbytes + self.scales.nbytes
+        return b + (self.biases.nbytes if self.biases is not None else 0)
+
+
+@dataclass
+class HostBlock:
+    """The tensors of one SparseMoe (moe.rs:109-147) on the host."""
+
+    shape: Shape
+    router: np.ndarray                 # [E, D] bf16
+    router_bias: np.ndarray | None     # [E] bf16
+    gate_proj: QTensor
+    up_proj: QTensor
+    down_proj: QTensor
+    sh_gate_proj: QTensor | None = None
+    sh_up_proj: QTensor | None = None
+    sh_down_proj: QTensor | None = None
+    sh_expert_gate: np.ndarray | None = None  # [1, D] bf16
+    zipf_rank: np.ndarray | None = field(default=None, repr=False)
+
+    @property
+    def nbytes(self) -> int:
+        n = self.router.nbytes + self.gate_proj.nbytes + self.up_proj.nbytes
+        n += self.down_proj.nbytes
+        for q in (self.sh_gate_proj, self.sh_up_proj, self.sh_down_proj):
+            if q is not None:
+                n += q.nbytes
+        if self.sh_expert_gate is not None:
+            n += self.sh_expert_gate.nbytes
+        return n
+
+
+_LIB = None
+
+
+def lib() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build()")
+        l = ctypes.CDLL(str(LIB_PATH))
+        l.mrun_synth_mix64.restype = c_uint64
+        l.mrun_synth_mix64.argtypes = [c_uint64]
+        l.mrun_synth_tensor_seed.restype = c_uint64
+        l.mrun_synth_tensor_seed.argtypes = [c_uint64, c_uint32, c_uint32, c_uint32]
+        l.mrun_synth_draw.restype = c_uint64
+        l.mrun_synth_draw.argtypes = [c_uint64, c_uint64]
+        l.mrun_synth_normal.restype = c_double
+        l.mrun_synth_normal.argtypes = [c_uint64, c_uint64]
+        l.mrun_synth_codes.restype = c_int32
+        l.mrun_synth_codes.argtypes = [c_uint64, c_int32, POINTER(c_uint32), c_size_t]
+        l.mrun_synth_normal_bf16.restype = None
+        l.mrun_synth_normal_bf16.argtypes = [c_uint64, c_float, POINTER(c_uint16), c_size_t]
+        l.mrun_synth_scales_biases.restype = None
+        l.mrun_synth_scales_biases.argtypes = [c_uint64, POINTER(c_uint16), POINTER(c_uint16),
+                                              c_size_t]
+        l.mrun_synth_zipf_bias.restype = c_int32
+        l.mrun_synth_zipf_bias.argtypes = [c_uint64, c_int32, c_double, c_double,
+                                          POINTER(c_uint16), POINTER(c_int32)]
+        _LIB = l
+    return _LIB
+
+
+def _p(a: np.ndarray, t):
+    return a.ctypes.data_as(POINTER(t))
+
+
+def seed(config: int, layer: int, tensor: int, base: int = BASE_SEED) -> int:
+    return int(lib().mrun_synth_tensor_seed(base, config, layer, tensor))
+
+
+def codes(s: int, n_words: int, bits: int = 4) -> np.ndarray:
+    out = np.empty(n_words, dtype=np.uint32)
+    if lib().mrun_synth_codes(s, bits, _p(out, c_uint32), n_words) != 0:
+        raise ValueError("bits must be 4 or 8")
+    return out
+
+
+def normal_bf16(s: int, n: int, std: float) -> np.ndarray:
+    out = np.empty(n, dtype=np.uint16)
+    lib().mrun_synth_normal_bf16(s, std, _p(out, c_uint16), n)
+    return out
+
+
+def scales_biases(s: int, n: int) -> tuple[np.ndarray, np.ndarray]:
+    sc = np.empty(n, dtype=np.uint16)
+    bi = np.empty(n, dtype=np.uint16)
+    lib().mrun_synth_scales_biases(s, _p(sc, c_uint16), _p(bi, c_uint16), n)
+    return sc, bi
+
+
+def zipf_bias(s: int, experts: int, exponent: float = 1.1, amp: float = 2.0):
+    b = np.empty(experts, dtype=np.uint16)
+    r = np.empty(experts, dtype=np.int32)
+    lib().mrun_synth_zipf_bias(s, experts, exponent, amp, _p(b, c_uint16), _p(r, c_int32))
+    return b, r
+
+
+def qtensor(config: int, layer: int, codes_id: int, scales_id: int, experts: int, out: int,
+            in_: int, group: int = 64) -> QTensor:
+    c = codes(seed(config, layer, codes_id), experts * out * in_ // 8)
+    sc, bi = scales_biases(seed(config, layer, scales_id), experts * out * in_ // group)
+    return QTensor(
+        codes=c.reshape(experts, out, in_ // 8),
+        scales=sc.reshape(experts, out, in_ // group),
+        biases=bi.reshape(experts, out, in_ // group),
+        experts=experts, out=out, in_=in_, group=group,
+    )
+
+
+def make_block(shape: Shape, config: int = CFG_DECODE, layer: int = 0,
+               zipf: bool = False) -> HostBlock:
+    D, E, I, S, g = shape.hidden, shape.experts, shape.intermediate, shape.shared, shape.group
+    router = normal_bf16(seed(config, layer, ROUTER_W), E * D, 0.02).reshape(E, D)
+    rb, rank = (None, None)
+    if zipf:
+        rb, rank = zipf_bias(seed(config, layer, ROUTER_BIAS), E)
+    blk = HostBlock(
+        shape=shape,
+        router=router,
+        router_bias=rb,
+        gate_proj=qtensor(config, layer, GATE_CODES, GATE_SCALES, E, I, D, g),
+        up_proj=qtensor(config, layer, UP_CODES, UP_SCALES, E, I, D, g),
+        down_proj=qtensor(config, layer, DOWN_CODES, DOWN_SCALES, E, D, I, g),
+        zipf_rank=rank,
+    )
+    if S:
+        blk.sh_gate_proj = qtensor(config, layer, SH_GATE_CODES, SH_GATE_SCALES, 1, S, D, g)
+        blk.sh_up_proj = qtensor(config, layer, SH_UP_CODES, SH_UP_SCALES, 1, S, D, g)
+        blk.sh_down_proj = qtensor(config, layer, SH_DOWN_CODES, SH_DOWN_SCALES, 1, D, S, g)
+        blk.sh_expert_gate = normal_bf16(seed(config, layer, SH_EXPERT_GATE), D, 0.02).reshape(1, D)
+    return blk
+
+
+def make_x(shape: Shape, tokens: int, config: int = CFG_DECODE, layer: int = 0) -> np.ndarray:
+    """bf16 N(0,1) activations [tokens, hidden]."""
+    return normal_bf16(seed(config, layer, X), tokens * shape.hidden, 1.0).reshape(
+        tokens, shape.hidden)
+
+
+def bf16_to_f32(a: np.ndarray) -> np.ndarray:
+    return (a.astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(a: np.ndarray) -> np.ndarray:
+    """Round to nearest even (NaN kept quiet)."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r

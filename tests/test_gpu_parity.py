@@ -1,0 +1,287 @@
+"""Parity of the HIP path (through the C ABI) with the CPU restatement on identical seeded inputs.
+
+Bars (the north star's): top-k ids and permutation indices bit-exact except where the router's
+bf16 values tie (within one ulp of the k-th boundary logit); block outputs within max-abs 2e-2 and
+L1-relative 1e-3 of the bf16 restatement, with f32 accumulation. Block outputs are compared with
+the oracle run on the GPU's own expert choice (validated as a top-k within ties first), so a tie
+broken the other way does not count as a numeric error.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from mrun_amd import moe as M
+from mrun_amd import synth
+from oracle import oracle as O
+from tests.helpers import assert_close, beyond_rounding, stats, ulp_distance
+
+pytestmark = pytest.mark.gpu
+
+SMALL = synth.Shape(hidden=256, experts=16, top_k=4, intermediate=128, shared=128)
+Q = synth.QWEN36
+
+
+def _log(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def q_host():
+    return synth.make_block(Q, config=synth.CFG_DECODE)
+
+
+@pytest.fixture(scope="module")
+def q_dev(q_host):
+    return M.SparseMoe(q_host)
+
+
+@pytest.fixture(scope="module")
+def small_host():
+    return synth.make_block(SMALL, config=synth.CFG_PLUMBING)
+
+
+@pytest.fixture(scope="module")
+def small_dev(small_host):
+    return M.SparseMoe(small_host)
+
+
+def run_block(hb, dev, x_np, label, check_rows=None):
+    """GPU forward vs oracle forward on the GPU's expert ids; returns (stats, tie-broken tokens)."""
+    T, k = x_np.shape[0], hb.shape.top_k
+    x = M.bf16_tensor(x_np)
+    out = dev.forward(x)
+    _, _, ids, _ = dev.router_forward(x)
+    torch.cuda.synchronize()
+    got = M.bf16_bits(out)
+    gids = M.u32_array(ids).reshape(T, k)
+    rows = np.arange(T) if check_rows is None else np.asarray(check_rows)
+    ref, tr = O.moe_forward(hb, x_np[rows], forced_ids=gids[rows], trace=True)
+    own = O.topk(tr["gates"], k)
+    ties = int(sum(set(a) != set(b) for a, b in zip(own.tolist(), gids[rows].tolist())))
+    s = assert_close(got[rows], ref, what=label)
+    _log(f"{label}: {s} tie-broken tokens {ties}/{len(rows)}")
+    return s, ties
+
+
+# ---------------------------------------------------------------------------------------------
+# router
+
+@pytest.mark.parametrize("T", [1, 2, 4, 16, 64, 2048])
+def test_router_matches_oracle(q_host, q_dev, T):
+    x_np = synth.make_x(Q, T, config=synth.CFG_DECODE, layer=T)
+    x = M.bf16_tensor(x_np)
+    logits, gates, ids, scores = q_dev.router_forward(x)
+    torch.cuda.synchronize()
+    lg, gg = M.bf16_bits(logits), M.bf16_bits(gates)
+    gi, gs = M.u32_array(ids).reshape(T, -1), M.bf16_bits(scores)
+    # logits: f32 accumulation in another order, so a rare one-ulp difference
+    ref_l = O.linear(q_host.router, x_np)
+    ul = ulp_distance(lg, ref_l)
+    assert beyond_rounding(lg, ref_l) == 0, f"logits differ by up to {ul.max()} ulps"
+    # the rest is checked on the GPU's own logits: softmax within one ulp (exp and sum order),
+    # ids exactly the top-k of the GPU's gates under the tie rule, scores bit-exact from them
+    ref_g = O.softmax(lg)
+    ug = ulp_distance(gg, ref_g)
+    assert ug.max() <= 1, f"gates differ by {ug.max()} ulps"
+    assert np.array_equal(gi, O.topk(gg, Q.top_k)), "ids are not the top-k of the gates"
+    assert np.array_equal(gs, O.scores(gg, gi, Q.norm_topk)), "scores differ"
+    # and against the oracle's own chain: ids equal except within-ulp ties
+    ref_gates_own = O.softmax(ref_l)
+    own = O.topk(ref_gates_own, Q.top_k)
+    diff = 0
+    for t in range(T):
+        if set(own[t]) != set(gi[t]):
+            diff += 1
+            assert O.topk_valid(ref_gates_own[t], ref_l[t], gi[t], ulps=1), f"token {t}"
+    _log(f"router T={T}: logits 1-ulp share {np.mean(ul > 0):.2e}, gates 1-ulp share "
+         f"{np.mean(ug > 0):.2e}, id sets differing within ties {diff}/{T}")
+
+
+# ---------------------------------------------------------------------------------------------
+# permute
+
+@pytest.mark.parametrize("T,k,E", [(1, 8, 256), (8, 8, 256), (16, 8, 256), (2048, 8, 256),
+                                   (8192, 8, 160), (20, 4, 16), (3000, 2, 512)])
+def test_permute_matches_oracle(T, k, E):
+    rng = np.random.default_rng(T * 131 + k * 7 + E)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.uint32)
+    dids = M.u32_tensor(ids)
+    offsets, order, inverse, token = M.permute(dids, k, E)
+    torch.cuda.synchronize()
+    r_order, r_inverse, r_token, r_counts = O.permute(ids, k, E)
+    assert np.array_equal(M.u32_array(order), r_order)
+    assert np.array_equal(M.u32_array(inverse), r_inverse)
+    assert np.array_equal(M.u32_array(token), r_token)
+    off = M.u32_array(offsets)
+    assert off[0] == 0 and np.array_equal(np.diff(off), r_counts)
+
+
+# ---------------------------------------------------------------------------------------------
+# products
+
+@pytest.mark.parametrize("n,x_rows,sorted_", [(8, 1, False), (16, 2, False), (64, 64, True),
+                                              (600, 600, False), (1024, 128, False)])
+def test_gather_qmm_matches_oracle(q_host, q_dev, n, x_rows, sorted_):
+    rng = np.random.default_rng(n + x_rows)
+    idx = rng.integers(0, Q.experts, n).astype(np.uint32)
+    if sorted_:
+        idx.sort()
+    x_np = synth.make_x(Q, x_rows, config=synth.CFG_DECODE, layer=1000 + n)
+    got = M.bf16_bits(M.gather_qmm(M.bf16_tensor(x_np), q_dev.gate_proj, M.u32_tensor(idx),
+                                   sorted_))
+    torch.cuda.synchronize()
+    ref = O.gather_qmm(q_host.gate_proj, x_np, idx)
+    s = assert_close(got, ref, max_ulp=1, what=f"gather_qmm n={n}")
+    _log(f"gather_qmm n={n} x_rows={x_rows}: {s}")
+
+
+@pytest.mark.parametrize("rows", [1, 7, 16, 300])
+def test_quantized_matmul_matches_oracle(q_host, q_dev, rows):
+    x_np = synth.make_x(Q, rows, config=synth.CFG_DECODE, layer=2000 + rows)
+    got = M.bf16_bits(M.quantized_matmul(M.bf16_tensor(x_np), q_dev.sh_gate_proj))
+    ref = O.qmatmul(q_host.sh_gate_proj, x_np)
+    s = assert_close(got, ref, max_ulp=1, what=f"quantized_matmul rows={rows}")
+    # down-shaped (K = 512)
+    a_np = synth.make_x(synth.Shape(512, 1, 1, 512), rows, config=9, layer=rows)
+    got2 = M.bf16_bits(M.quantized_matmul(M.bf16_tensor(a_np), q_dev.sh_down_proj))
+    ref2 = O.qmatmul(q_host.sh_down_proj, a_np)
+    s2 = assert_close(got2, ref2, max_ulp=1, what=f"quantized_matmul down rows={rows}")
+    _log(f"quantized_matmul rows={rows}: {s} / down {s2}")
+
+
+@pytest.mark.parametrize("rows", [3, 100])
+def test_linear_with_bias(rows):
+    zb, _ = synth.zipf_bias(5, 256)
+    w = synth.normal_bf16(11, 256 * 2048, 0.02).reshape(256, 2048)
+    x_np = synth.normal_bf16(12, rows * 2048, 1.0).reshape(rows, 2048)
+    got = M.bf16_bits(M.linear(M.bf16_tensor(x_np), M.bf16_tensor(w), M.bf16_tensor(zb)))
+    plain = M.bf16_bits(M.linear(M.bf16_tensor(x_np), M.bf16_tensor(w)))
+    # x W^T rounded once: within accumulation-order rounding of the oracle's
+    assert beyond_rounding(plain, O.linear(w, x_np)) == 0
+    # then the bias add, its own rounding (load.rs:302-305): bit-exact from the GPU's x W^T
+    want = synth.f32_to_bf16(synth.bf16_to_f32(plain) + synth.bf16_to_f32(zb)[None, :])
+    assert np.array_equal(got, want)
+
+
+def test_swiglu_combine_norm():
+    rng = np.random.default_rng(3)
+    g = synth.f32_to_bf16(rng.standard_normal(4096 + 5).astype(np.float32) * 3)
+    u = synth.f32_to_bf16(rng.standard_normal(4096 + 5).astype(np.float32))
+    got = M.bf16_bits(M.swiglu(M.bf16_tensor(g), M.bf16_tensor(u)))
+    assert ulp_distance(got, O.swiglu(g, u)).max() <= 1
+    T, k, D = 5, 8, 2048
+    y = synth.f32_to_bf16(rng.standard_normal((T * k, D)).astype(np.float32) * 0.02)
+    sc = synth.f32_to_bf16(rng.random((T, k)).astype(np.float32) / k)
+    sy = synth.f32_to_bf16(rng.standard_normal((T, D)).astype(np.float32) * 0.02)
+    gl = synth.f32_to_bf16(rng.standard_normal(T).astype(np.float32))
+    routed = O.combine(y, sc)
+    ref, _ = O.shared_add(routed, gl, sy)
+    got = M.bf16_bits(M.combine(M.bf16_tensor(y), M.bf16_tensor(sc), None, M.bf16_tensor(sy),
+                                M.bf16_tensor(gl)))
+    assert ulp_distance(got, ref).max() <= 1
+    got_r = M.bf16_bits(M.combine(M.bf16_tensor(y), M.bf16_tensor(sc)))
+    assert ulp_distance(got_r, routed).max() <= 1
+    x = synth.f32_to_bf16(rng.standard_normal((7, D)).astype(np.float32))
+    r = synth.f32_to_bf16(rng.standard_normal((7, D)).astype(np.float32))
+    w = synth.f32_to_bf16((1 + 0.1 * rng.standard_normal(D)).astype(np.float32))
+    got_n = M.bf16_bits(M.rms_norm(M.bf16_tensor(x), M.bf16_tensor(w), 1e-6))
+    assert ulp_distance(got_n, O.rms_norm(x, w, 1e-6)).max() <= 1
+    h, yv = M.add_rms_norm(M.bf16_tensor(x), M.bf16_tensor(r), M.bf16_tensor(w), 1e-6)
+    hs = synth.f32_to_bf16(synth.bf16_to_f32(x) + synth.bf16_to_f32(r))
+    assert np.array_equal(M.bf16_bits(h), hs)
+    assert ulp_distance(M.bf16_bits(yv), O.rms_norm(hs, w, 1e-6)).max() <= 1
+
+
+# ---------------------------------------------------------------------------------------------
+# the block
+
+@pytest.mark.parametrize("T", [1, 2, 4, 16])
+def test_block_decode_matches_oracle(q_host, q_dev, T):
+    x_np = synth.make_x(Q, T, config=synth.CFG_DECODE, layer=T)
+    run_block(q_host, q_dev, x_np, f"Q decode T={T}")
+
+
+@pytest.mark.parametrize("T", [1, 3, 20, 100])
+def test_block_small_shape(small_host, small_dev, T):
+    x_np = synth.make_x(SMALL, T, config=synth.CFG_PLUMBING, layer=T)
+    run_block(small_host, small_dev, x_np, f"small T={T}")
+
+
+def test_block_plumbing_config(q_host, q_dev):
+    """T = 16, 128 pairs (the sorted dispatch of the reference)."""
+    x_np = synth.make_x(Q, 16, config=synth.CFG_PLUMBING)
+    run_block(q_host, q_dev, x_np, "Q configs[0] T=16")
+
+
+@pytest.mark.parametrize("T", [17, 64, 300])
+def test_block_prefill_small(q_host, q_dev, T):
+    x_np = synth.make_x(Q, T, config=synth.CFG_PREFILL_ZIPF, layer=T)
+    run_block(q_host, q_dev, x_np, f"Q prefill T={T}")
+
+
+def test_block_prefill_zipf_2048():
+    """T = 2048 with the Zipf-biased router; hot expert load >= 10x the mean."""
+    hb = synth.make_block(Q, config=synth.CFG_PREFILL_ZIPF, zipf=True)
+    dev = M.SparseMoe(hb)
+    x_np = synth.make_x(Q, 2048, config=synth.CFG_PREFILL_ZIPF)
+    _, _, ids, _ = dev.router_forward(M.bf16_tensor(x_np))
+    counts = np.bincount(M.u32_array(ids).ravel(), minlength=Q.experts)
+    assert counts.max() >= 10 * counts.mean(), counts.max()
+    rows = np.random.default_rng(0).choice(2048, 256, replace=False)
+    run_block(hb, dev, x_np, "Q configs[2] T=2048 (256 sampled rows)", check_rows=np.sort(rows))
+    _log(f"zipf: hottest expert {counts.max()} pairs = {counts.max() / counts.mean():.1f}x mean")
+
+
+def test_rows_keep_their_one_row_bits(q_dev):
+    """A decode batch of T <= 16 rows gives every row the bits of its one-row product
+    (with_row_exact, nuvec.rs:256-265; lanes.rs:68-112)."""
+    x_np = synth.make_x(Q, 16, config=synth.CFG_DECODE, layer=77)
+    batch = M.bf16_bits(q_dev.forward(M.bf16_tensor(x_np)))
+    for T in (8, 16):
+        b = M.bf16_bits(q_dev.forward(M.bf16_tensor(x_np[:T])))
+        assert np.array_equal(b, batch[:T])
+    for t in range(16):
+        one = M.bf16_bits(q_dev.forward(M.bf16_tensor(x_np[t:t + 1])))
+        assert np.array_equal(one[0], batch[t]), f"row {t}"
+
+
+def test_forward_is_deterministic(q_dev):
+    x = M.bf16_tensor(synth.make_x(Q, 512, config=synth.CFG_DECODE, layer=5))
+    a = M.bf16_bits(q_dev.forward(x))
+    b = M.bf16_bits(q_dev.forward(x))
+    assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("T", [1, 8])
+def test_block_coder_decode(T):
+    """configs[4] at decode: hidden 6144, 160 experts, FFN 2560, no shared expert."""
+    hb = _coder_host()
+    dev = _coder_dev()
+    x_np = synth.make_x(synth.CODER, T, config=synth.CFG_CODER, layer=T)
+    run_block(hb, dev, x_np, f"Coder decode T={T}")
+
+
+def test_block_coder_prefill_rows():
+    T = 1024
+    hb = _coder_host()
+    dev = _coder_dev()
+    x_np = synth.make_x(synth.CODER, T, config=synth.CFG_CODER, layer=T)
+    rows = np.random.default_rng(1).choice(T, 32, replace=False)
+    run_block(hb, dev, x_np, f"Coder prefill T={T} (32 sampled rows)", check_rows=np.sort(rows))
+
+
+_CODER = {}
+
+
+def _coder_host():
+    if "host" not in _CODER:
+        _CODER["host"] = synth.make_block(synth.CODER, config=synth.CFG_CODER)
+    return _CODER["host"]
+
+
+def _coder_dev():
+    if "dev" not in _CODER:
+        _CODER["dev"] = M.SparseMoe(_coder_host())
+    return _CODER["dev"]
