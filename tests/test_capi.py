@@ -1,0 +1,118 @@
+"""The C-ABI library (include/*.h) loads and exports every declared entry point, and its host-side
+validation reports errors the way the facade does (status + message). No GPU: no call here
+reaches device work."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from mrun_amd import _lib
+from mrun_amd._lib import Linear, MoeConfig, Quantized, SparseMoe
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def declared(header: Path) -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(mrun_\w+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported():
+    lib = _lib.load()
+    names = declared(ROOT / "include" / "mrun_moe.h")
+    assert len(names) >= 15
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_lib.SIGNATURES), "the ctypes view must cover the header"
+    syn = ctypes.CDLL(str(ROOT / "mrun_amd" / "lib" / "libmrun_synth.so"))
+    for n in declared(ROOT / "include" / "mrun_synth.h"):
+        assert hasattr(syn, n), n
+    assert b"gfx950" in lib.mrun_version()
+
+
+FAKE = 1 << 20  # a 16-byte aligned address no check dereferences
+
+
+def q(experts, out, in_, group=64, bits=4, ptr=FAKE):
+    return Quantized(ptr, ptr, ptr, experts, out, in_, group, bits)
+
+
+def block(D=2048, E=256, k=8, I=512, S=512, **over):
+    m = SparseMoe()
+    m.cfg = MoeConfig(D, E, k, I, 1, S)
+    m.gate = Linear(FAKE, Quantized(), None, E, D)
+    m.switch_gate_proj = q(E, I, D)
+    m.switch_up_proj = q(E, I, D)
+    m.switch_down_proj = q(E, D, I)
+    if S:
+        m.shared_gate_proj = Linear(None, q(1, S, D), None, S, D)
+        m.shared_up_proj = Linear(None, q(1, S, D), None, S, D)
+        m.shared_down_proj = Linear(None, q(1, D, S), None, D, S)
+        m.shared_expert_gate = Linear(FAKE, Quantized(), None, 1, D)
+    for k_, v in over.items():
+        setattr(m, k_, v)
+    return m
+
+
+def status(m):
+    lib = _lib.load()
+    rc = lib.mrun_moe_check(ctypes.byref(m))
+    return rc, lib.mrun_last_error().decode()
+
+
+def test_valid_blocks_pass():
+    assert status(block()) == (0, "")
+    assert status(block(D=6144, E=160, I=2560, S=0)) == (0, "")
+
+
+@pytest.mark.parametrize("over,code,text", [
+    ({"switch_gate_proj": q(256, 512, 2048, group=16)}, _lib.MRUN_ERR_INVALID, "group size 16"),
+    ({"switch_gate_proj": q(256, 512, 2048, bits=3)}, _lib.MRUN_ERR_INVALID, "3 bits"),
+    ({"switch_gate_proj": q(256, 512, 2048, bits=8)}, _lib.MRUN_ERR_UNSUPPORTED, "8-bit"),
+    ({"switch_down_proj": q(256, 512, 2048)}, _lib.MRUN_ERR_INVALID, "down_proj: shape"),
+    ({"switch_up_proj": q(256, 512, 2048, ptr=FAKE + 4)}, _lib.MRUN_ERR_INVALID, "aligned"),
+    ({"gate": Linear(None, q(256, 256, 2048), None, 256, 2048)}, _lib.MRUN_ERR_UNSUPPORTED,
+     "quantized routers"),
+])
+def test_invalid_blocks_are_refused(over, code, text):
+    rc, msg = status(block(**over))
+    assert rc == code and text in msg, (rc, msg)
+
+
+def test_top_k_must_fit_the_experts():
+    m = block()
+    m.cfg = MoeConfig(2048, 256, 257, 512, 1, 512)
+    rc, msg = status(m)
+    assert rc == _lib.MRUN_ERR_INVALID and "num_experts_per_tok" in msg
+
+
+def test_workspace_contract():
+    lib = _lib.load()
+    cfg = MoeConfig(2048, 256, 8, 512, 1, 512)
+    sizes = [lib.mrun_moe_workspace_bytes(ctypes.byref(cfg), t) for t in (1, 16, 2048)]
+    assert 0 < sizes[0] < sizes[1] < sizes[2]
+    # below SparseMoe::scratch_per_token (moe.rs:176-187: 188,416 B per token here)
+    assert sizes[2] < 2048 * 188416
+    assert lib.mrun_moe_workspace_bytes(ctypes.byref(MoeConfig(0, 0, 0, 0, 0, 0)), 4) == 0
+    # a workspace one byte short is refused before any device work
+    m = block()
+    rc = lib.mrun_moe_forward(ctypes.byref(m), FAKE, 1, FAKE * 2, FAKE * 4, sizes[0] - 1, None)
+    assert rc == _lib.MRUN_ERR_WORKSPACE and "workspace" in lib.mrun_last_error().decode()
+    rc = lib.mrun_moe_forward(ctypes.byref(m), FAKE, 1, FAKE, FAKE * 4, sizes[0], None)
+    assert rc == _lib.MRUN_ERR_INVALID and "alias" in lib.mrun_last_error().decode()
+    rc = lib.mrun_moe_forward(ctypes.byref(m), FAKE, 0, FAKE * 2, FAKE * 4, sizes[0], None)
+    assert rc == _lib.MRUN_ERR_INVALID
+
+
+def test_op_argument_errors():
+    lib = _lib.load()
+    rc = lib.mrun_moe_permute(FAKE, 10, 3, 16, FAKE, None, None, None, None, 0, None)
+    assert rc == _lib.MRUN_ERR_INVALID and "multiple of top_k" in lib.mrun_last_error().decode()
+    rc = lib.mrun_moe_combine(FAKE, None, FAKE, 2, 8, 2050, None, None, FAKE, None)
+    assert rc == _lib.MRUN_ERR_INVALID
+    w = q(4, 64, 100)
+    rc = lib.mrun_gather_qmm(FAKE, 2, ctypes.byref(w), FAKE, 4, 0, FAKE, FAKE, 1 << 20, None)
+    assert rc == _lib.MRUN_ERR_INVALID and "scale groups" in lib.mrun_last_error().decode()
