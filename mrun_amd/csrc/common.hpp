@@ -23,28 +23,76 @@ __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 
 __device__ __forceinline__ float sigmoidf_(float z) { return 1.0f / (1.0f + expf(-z)); }
 
-// Sum over the lanes of groups of `width` consecutive lanes (width a power of two <= 64);
-// every lane of the group receives the total. Fixed butterfly order: deterministic.
+// Cross-lane reductions without the LDS crossbar: DPP moves combine lanes inside each 16-lane row
+// (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror: every lane of a row
+// ends with the row's total), then v_readlane gathers the rows' totals into scalars. The order of
+// the additions is fixed, so results are deterministic.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __uint_as_float(dpp_u32<CTRL>(__float_as_uint(v)));
+}
+__device__ __forceinline__ float lane_f32(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+__device__ __forceinline__ float row_sum16(float v) {
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x141>(v);
+    v += dpp_f32<0x140>(v);
+    return v;
+}
+
+// Sum over groups of WIDTH consecutive lanes (16, 32 or 64); every lane of a group receives its
+// group's total.
 template <int WIDTH>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int m = WIDTH / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-    return v;
+    static_assert(WIDTH == 1 || WIDTH == 2 || WIDTH == 4 || WIDTH == 8 || WIDTH == 16 ||
+                      WIDTH == 32 || WIDTH == 64,
+                  "group width");
+    if (WIDTH == 1) return v;
+    if (WIDTH == 2) return v + dpp_f32<0xB1>(v);
+    if (WIDTH == 4) {
+        v += dpp_f32<0xB1>(v);
+        return v + dpp_f32<0x4E>(v);
+    }
+    if (WIDTH == 8) {
+        v += dpp_f32<0xB1>(v);
+        v += dpp_f32<0x4E>(v);
+        return v + dpp_f32<0x141>(v);
+    }
+    v = row_sum16(v);
+    if (WIDTH == 16) return v;
+    const float r0 = lane_f32(v, 0), r1 = lane_f32(v, 16), r2 = lane_f32(v, 32),
+                r3 = lane_f32(v, 48);
+    if (WIDTH == 32) return (threadIdx.x & 32) ? r2 + r3 : r0 + r1;
+    return (r0 + r1) + (r2 + r3);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-    return v;
+    v = fmaxf(v, dpp_f32<0xB1>(v));
+    v = fmaxf(v, dpp_f32<0x4E>(v));
+    v = fmaxf(v, dpp_f32<0x141>(v));
+    v = fmaxf(v, dpp_f32<0x140>(v));
+    return fmaxf(fmaxf(lane_f32(v, 0), lane_f32(v, 16)), fmaxf(lane_f32(v, 32), lane_f32(v, 48)));
 }
 
+__device__ __forceinline__ uint32_t umax_(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        uint32_t o = (uint32_t)__shfl_xor((int)v, m, 64);
-        v = o > v ? o : v;
-    }
-    return v;
+    v = umax_(v, dpp_u32<0xB1>(v));
+    v = umax_(v, dpp_u32<0x4E>(v));
+    v = umax_(v, dpp_u32<0x141>(v));
+    v = umax_(v, dpp_u32<0x140>(v));
+    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+    const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+    const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return umax_(umax_(r0, r1), umax_(r2, r3));
 }
 
 // Eight bf16 (one uint4) dotted with eight f32 codes.

@@ -1,0 +1,138 @@
+// Inner loop of the decode-shaped 4-bit products: one wave streams weight rows with 128-bit loads
+// and dots them with a few activation rows, dequantizing in registers.
+//
+// Dequant: nibble q sits in the low mantissa bits of bf16 128.0 (0x4300 | q == 128 + q exactly),
+// so two codes of a word become a bf16 pair with one and-or. The pair holds codes (i, i + 4) of
+// the word, and the activations are re-paired the same way once per row (v_perm_b32); v_dot2
+// then accumulates x * (128 + q) in f32 and the affine map folds the offset back:
+//     sum_k x_k (q_k s + b) = s * sum_k x_k (128 + q_k) + (b - 128 s) * sum_k x_k.
+// A lane owns 32-code chunks li, li + LPR, ...; a chunk lies in one quant group (32 | group). The
+// LPR lanes of a row are summed by a fixed butterfly, so a row's bits depend on K only.
+#pragma once
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace mrun {
+
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                           __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// 32 activations re-paired as (x[8w+i], x[8w+i+4]) in dword 4w+i, and their sum.
+struct XChunk {
+    uint32_t v[16];
+    float sum;
+};
+
+// 32 activations as loaded (4 x 128 bits).
+struct XRaw {
+    uint4 a[4];
+};
+
+__device__ __forceinline__ void load_xraw(const bf16_t *src, XRaw &r) {
+    const uint4 *p = (const uint4 *)src;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) r.a[w] = p[w];
+}
+
+__device__ __forceinline__ void pair_x(const XRaw &r, XChunk &c) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint4 a = r.a[w];
+        c.v[4 * w + 0] = __builtin_amdgcn_perm(a.z, a.x, 0x05040100u);
+        c.v[4 * w + 1] = __builtin_amdgcn_perm(a.z, a.x, 0x07060302u);
+        c.v[4 * w + 2] = __builtin_amdgcn_perm(a.w, a.y, 0x05040100u);
+        c.v[4 * w + 3] = __builtin_amdgcn_perm(a.w, a.y, 0x07060302u);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s = dot2(c.v[i], 0x3F803F80u, s);
+    c.sum = s;
+}
+
+// sum_k x_k (128 + q_k) over the 32 codes of one uint4.
+__device__ __forceinline__ float dot_chunk(const uint4 &q, const XChunk &x) {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        acc = dot2(x.v[4 * i + 0], (w[i] & 0x000F000Fu) | 0x43004300u, acc);
+        acc = dot2(x.v[4 * i + 1], ((w[i] >> 4) & 0x000F000Fu) | 0x43004300u, acc);
+        acc = dot2(x.v[4 * i + 2], ((w[i] >> 8) & 0x000F000Fu) | 0x43004300u, acc);
+        acc = dot2(x.v[4 * i + 3], ((w[i] >> 12) & 0x000F000Fu) | 0x43004300u, acc);
+    }
+    return acc;
+}
+
+// One weight row's chunks for one lane: codes and the raw bf16 scale and bias. Loads use clamped
+// addresses and are never followed by a use inside a condition, so all of a wave's loads are in
+// flight together; `ok` masks the chunks that lie past the row or the matrix.
+template <int CPL>
+struct WRow {
+    uint4 q[CPL];
+    uint32_t s[CPL], b[CPL];
+    uint32_t ok;
+};
+
+template <int CPL>
+__device__ __forceinline__ void load_wrow(const QW &w, int e, int row, int li, int lpr,
+                                          WRow<CPL> &r) {
+    const int n_ch = w.in >> 5;
+    const int groups = w.in / w.group;
+    const size_t rr = (size_t)e * w.out + min(row, w.out - 1);
+    const uint32_t *codes = w.codes + rr * (size_t)(w.in >> 3);
+    r.ok = 0;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int ch = li + c * lpr;
+        const int chc = min(ch, n_ch - 1);
+        r.q[c] = *(const uint4 *)(codes + (size_t)chc * 4);
+        const size_t gi = rr * groups + (chc * 32) / w.group;
+        r.s[c] = w.scales[gi];
+        r.b[c] = w.biases ? (uint32_t)w.biases[gi] : 0u;
+        r.ok |= (row < w.out && ch < n_ch) ? (1u << c) : 0u;
+    }
+}
+
+// Lane's part of row . x over its chunks: s * sum x (128 + q) + (b - 128 s) * sum x.
+template <int CPL>
+__device__ __forceinline__ float row_part(const WRow<CPL> &r, const XChunk *x) {
+    float a = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const bool ok = (r.ok >> c) & 1u;
+        const float s = ok ? bf2f(r.s[c]) : 0.f;
+        const float bp = ok ? bf2f(r.b[c]) - 128.f * s : 0.f;
+        a += s * dot_chunk(r.q[c], x[c]) + bp * x[c].sum;
+    }
+    return a;
+}
+
+// Keeps packed codes opaque inside a loop so their conversion is not hoisted out of it.
+template <int CPL>
+__device__ __forceinline__ void opaque_row(WRow<CPL> &r) {
+#pragma unroll
+    for (int c = 0; c < CPL; ++c)
+        asm volatile("" : "+v"(r.q[c].x), "+v"(r.q[c].y), "+v"(r.q[c].z), "+v"(r.q[c].w));
+}
+
+// The lane's chunks of one activation row (clamped: chunks past the row are masked by the
+// weights' `ok`, so their values never count).
+template <int CPL>
+__device__ __forceinline__ void load_xrow_raw(const bf16_t *row, int li, int lpr, int n_ch,
+                                              XRaw *x) {
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) load_xraw(row + min(li + c * lpr, n_ch - 1) * 32, x[c]);
+}
+
+template <int CPL>
+__device__ __forceinline__ void pair_xrow(const XRaw *raw, XChunk *x) {
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) pair_x(raw[c], x[c]);
+}
+
+}  // namespace mrun

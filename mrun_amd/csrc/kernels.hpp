@@ -29,17 +29,26 @@ struct Routing {
     const uint32_t *n_tiles;
 };
 
+// Benchmark instrumentation: an event recorded on the stream after each stage of a forward.
+struct StageMarks {
+    hipEvent_t *events = nullptr;
+    int n_events = 0;
+    int count = 0;
+    void mark(hipStream_t s) {
+        if (events && count + 1 < n_events) (void)hipEventRecord(events[count + 1], s);
+        ++count;
+    }
+};
+
 // ---- router ----
 
-// logits[t][r] = R(x[t] . W[r]) then, with bias, R(logit + bias[r]) for r < E, t < T <= 16.
-// With xw (one extra weight row [D]) the extra block writes xout[t] = R(x[t] . xw).
-hipError_t launch_router_gemv(const bf16_t *x, int T, int D, const bf16_t *W, const bf16_t *bias,
-                              int E, bf16_t *logits, const bf16_t *xw, bf16_t *xout,
-                              hipStream_t stream);
+// Dense Linear for T <= 16 rows: out[t][r] = R(x[t] . W[r]) then, with bias, R(. + bias[r]); one
+// wave per output row, a token's accumulation order independent of T.
+hipError_t launch_rows(const bf16_t *x, int T, int D, const bf16_t *W, const bf16_t *bias, int N,
+                       bf16_t *out, hipStream_t stream);
 
 // Softmax (f32, one rounding), top-k (equal gates: lower id first; ids in rank order) and
-// scores (normalised when norm) for T tokens; gates optional. With permute outputs given
-// (decode: T*k <= 1024), the same launch also runs the stable permute.
+// scores (normalised when norm) for T tokens; gates optional.
 struct PermuteOut {
     uint32_t *offsets;   // [E+1]
     uint32_t *order;     // [P] or null
@@ -52,12 +61,21 @@ struct PermuteOut {
     int tile_m;          // rows per tile
 };
 hipError_t launch_topk(const bf16_t *logits, int T, int E, int k, bool norm, bf16_t *gates,
-                       uint32_t *ids, bf16_t *scores, const PermuteOut *fused_permute,
-                       hipStream_t stream);
+                       uint32_t *ids, bf16_t *scores, hipStream_t stream);
 
 // Stable counting sort of ids [P] (values < E) by expert (one workgroup).
 hipError_t launch_permute(const uint32_t *ids, int P, int k, int E, const PermuteOut &out,
                           hipStream_t stream);
+
+// Prefill routing in two launches over many workgroups: top-k + per-workgroup histograms that
+// reserve ranges in counts[E] (zero on entry) with one atomic per (workgroup, expert), then a
+// scatter that places every pair inside its expert's range. Rows of an expert are contiguous but
+// not in token order; every row's result is independent of its position.
+hipError_t launch_topk_rank(const bf16_t *logits, int T, int E, int k, bool norm, uint32_t *ids,
+                            bf16_t *scores, uint32_t *counts, uint32_t *rank,
+                            hipStream_t stream);
+hipError_t launch_scatter(const uint32_t *ids, const uint32_t *rank, const uint32_t *counts,
+                          int P, int k, int E, const PermuteOut &out, hipStream_t stream);
 
 // ---- products ----
 
@@ -91,25 +109,24 @@ struct GemvJob {
 };
 hipError_t launch_gemv(const GemvJob &job, hipStream_t stream);
 
-// Decode down projection fused with the combine (moe.rs:84-93, 161-171): for each output row d,
-// every active expert's pairs (act rows at sorted positions) and the shared expert's rows, then
-// out[t][d] = R(R(sum_j R(y[inverse[t*k+j]][d] * scores[t][j])) + R(R(sigmoid(sh_logit[t])) *
-// ysh[t][d])). T*k <= 128.
-struct DownCombineJob {
-    const bf16_t *act;   // [P, I] sorted positions
-    QW wd;               // [E, D, I]
-    Routing routing;
-    int max_slots;
-    const uint32_t *inverse;
-    const bf16_t *scores;
-    int T, k;
-    int has_shared;
-    const bf16_t *sh_act; // [T, I_s]
-    QW swd;               // [1, D, I_s]
-    const bf16_t *sh_logit;
-    bf16_t *out;          // [T, D]
+// The decode schedule (decode.hip): router + shared expert gate/up, routed gate/up, down +
+// combine, for T <= 16 tokens and T*k <= 128 pairs.
+struct DecodeJob {
+    const bf16_t *x;
+    int T, D, E, k, I, S, norm, max_slots;
+    const bf16_t *router, *router_bias, *sh_gate_w, *sh_gate_b;
+    QW wg, wu, wd, sg, su, sd;
+    bf16_t *logits;   // [T, E]
+    uint32_t *ids;    // [T, k] and
+    bf16_t *scores;   // [T, k]: the routing, computed once by a top-k launch when T > 4
+    int topk_in_kernel;  // T <= 4: each workgroup re-derives the top-k from the logits instead
+    bf16_t *sh_logit; // [T]
+    bf16_t *sh_act;   // [T, S]
+    bf16_t *act;      // [T*k, I], pair p = t*k + j
+    bf16_t *out;      // [T, D]
 };
-hipError_t launch_down_combine(const DownCombineJob &job, hipStream_t stream);
+bool decode_supported(int D, int I, int S, int T, int k, int E);
+hipError_t launch_decode(const DecodeJob &job, hipStream_t stream, StageMarks *marks);
 
 // MFMA bf16 grouped GEMM (prefill): rows at sorted positions grouped in tiles (routing.tiles) or,
 // without routing, M rows of expert 0. B is quantized (w0, and w1 with glu) or dense bf16 bd
@@ -131,6 +148,8 @@ struct GemmJob {
     bf16_t *out;
     int ldo;
     int glu;
+    uint32_t *zero;  // block (0, 0) clears zero[0..n_zero) (routing counters of the next launch)
+    int n_zero;
 };
 hipError_t launch_gemm(const GemmJob &job, hipStream_t stream);
 constexpr int kGemmTileM = 64;

@@ -151,6 +151,7 @@ static Status check_block(const mrun_sparse_moe *m) {
 
 struct Plan {
     size_t logits, ids, scores, offsets, order, inverse, token, active, n_active, tiles, n_tiles;
+    size_t counts, rank;
     size_t act, y, sh_logit, sh_act, sh_y, total;
     int max_tiles;
 };
@@ -179,6 +180,8 @@ static Plan make_plan(const mrun_moe_config &c, int T) {
     p.n_active = take(4);
     p.tiles = take(12 * (size_t)p.max_tiles);
     p.n_tiles = take(4);
+    p.counts = take(4 * E);
+    p.rank = take(4 * P);
     p.act = take(2 * P * I);
     p.y = take(2 * P * D);
     if (S > 0) {
@@ -197,7 +200,7 @@ namespace tensor {
 
 // Linear::forward with a dense bf16 weight (load.rs:294-306): y = R(x W^T), then R(y + bias).
 static Status linear_dense(const bf16_t *x, int rows, const mrun_linear &l, bf16_t *y,
-                           hipStream_t s) {
+                           hipStream_t s, uint32_t *zero = nullptr, int n_zero = 0) {
     const int N = l.out, K = l.in;
     if (K % 8 != 0) return Err(MRUN_ERR_UNSUPPORTED, "linear: input width must be a multiple of 8");
     if (rows > 16 && N < 16) {
@@ -208,14 +211,14 @@ static Status linear_dense(const bf16_t *x, int rows, const mrun_linear &l, bf16
         GemmJob j{};
         j.A = x, j.lda = K, j.a_div = 1, j.M = rows, j.N = N, j.K = K;
         j.bd = l.weight, j.bias = l.bias, j.out = y, j.ldo = N;
+        j.zero = zero, j.n_zero = n_zero;
         TRY_HIP(launch_gemm(j, s), "linear (mfma)");
         return Ok();
     }
     for (int r0 = 0; r0 < rows; r0 += 16) {
         const int n = rows - r0 < 16 ? rows - r0 : 16;
-        TRY_HIP(launch_router_gemv(x + (size_t)r0 * K, n, K, l.weight, l.bias, N,
-                                   y + (size_t)r0 * N, nullptr, nullptr, s),
-                "linear (gemv)");
+        TRY_HIP(launch_rows(x + (size_t)r0 * K, n, K, l.weight, l.bias, N, y + (size_t)r0 * N, s),
+                "linear (rows)");
     }
     return Ok();
 }
@@ -246,12 +249,11 @@ static Status linear(const bf16_t *x, int rows, const mrun_linear &l, bf16_t *y,
 
 // Router: logits = gate(x); gates = softmax; ids = top-k; scores (moe.rs:151-159).
 static Status router(const mrun_sparse_moe &m, const bf16_t *x, int T, bf16_t *logits,
-                     bf16_t *gates, uint32_t *ids, bf16_t *scores, const PermuteOut *fused,
-                     hipStream_t s) {
+                     bf16_t *gates, uint32_t *ids, bf16_t *scores, hipStream_t s) {
     const mrun_moe_config &c = m.cfg;
     TRY(linear_dense(x, T, m.gate, logits, s));
     TRY_HIP(launch_topk(logits, T, c.experts, c.top_k, c.norm_topk_prob != 0, gates, ids, scores,
-                        fused, s),
+                        s),
             "router top-k");
     return Ok();
 }
@@ -260,25 +262,15 @@ static Status router(const mrun_sparse_moe &m, const bf16_t *x, int T, bf16_t *l
 
 namespace models {
 
-// Benchmark instrumentation: an event recorded on the stream after each stage of the forward.
-struct Stages {
-    hipEvent_t *events = nullptr;
-    int n_events = 0;
-    int count = 0;
-    void mark(hipStream_t s) {
-        if (events && count + 1 < n_events) (void)hipEventRecord(events[count + 1], s);
-        ++count;
-    }
-};
+using Stages = StageMarks;
 
-static const char *kDecodeStages = "router,topk_permute,gate_up,down_combine";
+static const char *kDecodeStages = "router_shared,gate_up,down_combine";
 static const char *kPrefillStages =
     "router,shared_gate,topk,permute,gate_up,down,shared_gate_up,shared_down,combine";
 
 static bool is_decode(const mrun_moe_config &c, int T) {
-    const int I = c.intermediate, S = c.shared_intermediate;
-    // the fused down + combine kernel keeps T*k <= 128 pairs in LDS and needs rows of >= 256 codes
-    return T <= 16 && T * c.top_k <= 128 && I >= 256 && (S == 0 || S >= 256);
+    return decode_supported(c.hidden, c.intermediate, c.shared_intermediate, T, c.top_k,
+                            c.experts);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -322,53 +314,38 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
     const bool mfma = D % 64 == 0 && I % 64 == 0 && (S == 0 || S % 64 == 0);  // K of each product
 
     if (decode) {
-        // 1. router logits (+ the shared expert's gate logit in the same launch)
-        TRY_HIP(launch_router_gemv(x, T, D, m.gate.weight, m.gate.bias, E, logits,
-                                   S ? m.shared_expert_gate.weight : nullptr, sh_logit, s),
-                "router");
-        if (S && m.shared_expert_gate.bias)
-            TRY_HIP(launch_add_bias(sh_logit, m.shared_expert_gate.bias, T, 1, s), "gate bias");
-        st.mark(s);
-        // 2. softmax, top-k, scores and the stable permute in one workgroup
-        TRY_HIP(launch_topk(logits, T, E, k, c.norm_topk_prob != 0, nullptr, ids, scores, &po, s),
-                "top-k");
-        st.mark(s);
-        // 3. gate/up + swiglu for every active expert, and the shared expert's gate/up
-        GemvJob g{};
-        g.A = x, g.lda = D, g.a_map = po.order, g.a_div = k;
-        g.w0 = qw_of(m.switch_gate_proj), g.w1 = qw_of(m.switch_up_proj);
-        g.routing = rt, g.has_routing = 1, g.max_slots = max_slots;
-        g.out = act, g.ldo = I, g.glu = 1;
+        DecodeJob j{};
+        j.x = x, j.T = T, j.D = D, j.E = E, j.k = k, j.I = I, j.S = S;
+        j.norm = c.norm_topk_prob != 0, j.max_slots = max_slots;
+        j.router = m.gate.weight, j.router_bias = m.gate.bias;
+        j.wg = qw_of(m.switch_gate_proj), j.wu = qw_of(m.switch_up_proj);
+        j.wd = qw_of(m.switch_down_proj);
         if (S) {
-            g.xA = x, g.x_lda = D, g.xw0 = qw_of(m.shared_gate_proj.q);
-            g.xw1 = qw_of(m.shared_up_proj.q), g.x_rows = T, g.xout = sh_act, g.x_ldo = S;
+            j.sh_gate_w = m.shared_expert_gate.weight, j.sh_gate_b = m.shared_expert_gate.bias;
+            j.sg = qw_of(m.shared_gate_proj.q), j.su = qw_of(m.shared_up_proj.q);
+            j.sd = qw_of(m.shared_down_proj.q);
         }
-        TRY_HIP(launch_gemv(g, s), "gate/up");
-        st.mark(s);
-        // 4. down projection fused with the weighted combine and the gated shared expert
-        DownCombineJob dj{};
-        dj.act = act, dj.wd = qw_of(m.switch_down_proj), dj.routing = rt;
-        dj.max_slots = max_slots, dj.inverse = po.inverse, dj.scores = scores, dj.T = T, dj.k = k;
-        dj.has_shared = S > 0, dj.sh_act = sh_act;
-        if (S) dj.swd = qw_of(m.shared_down_proj.q);
-        dj.sh_logit = sh_logit, dj.out = out;
-        TRY_HIP(launch_down_combine(dj, s), "down/combine");
-        st.mark(s);
+        j.logits = logits, j.sh_logit = sh_logit, j.sh_act = sh_act, j.act = act, j.out = out;
+        j.ids = ids, j.scores = scores, j.topk_in_kernel = T <= 4;
+        TRY_HIP(launch_decode(j, s, &st), "decode");
         return Ok();
     }
 
     // prefill
-    TRY(tensor::linear_dense(x, T, m.gate, logits, s));
+    uint32_t *counts = (uint32_t *)at(p.counts), *rank = (uint32_t *)at(p.rank);
+    const bool mfma_router = T > 16 && E >= 16 && D % 64 == 0;  // linear_dense's MFMA branch
+    if (!mfma_router) TRY_HIP(hipMemsetAsync(counts, 0, 4 * (size_t)E, s), "clear counts");
+    TRY(tensor::linear_dense(x, T, m.gate, logits, s, mfma_router ? counts : nullptr, E));
     st.mark(s);
     if (S) TRY(tensor::linear_dense(x, T, m.shared_expert_gate, sh_logit, s));
     st.mark(s);
-    TRY_HIP(launch_topk(logits, T, E, k, c.norm_topk_prob != 0, nullptr, ids, scores, nullptr, s),
+    TRY_HIP(launch_topk_rank(logits, T, E, k, c.norm_topk_prob != 0, ids, scores, counts, rank, s),
             "top-k");
     st.mark(s);
     PermuteOut pt = po;
     pt.tiles = (uint32_t *)at(p.tiles);
     pt.n_tiles = (uint32_t *)at(p.n_tiles);
-    TRY_HIP(launch_permute(ids, P, k, E, pt, s), "permute");
+    TRY_HIP(launch_scatter(ids, rank, counts, P, k, E, pt, s), "scatter");
     st.mark(s);
     if (mfma) {
         GemmJob g{};
@@ -475,7 +452,7 @@ int mrun_moe_forward_profiled(const mrun_sparse_moe *moe, const mrun_bf16 *x, in
     if (st.ok()) st = check_ptr(out, "out");
     if (st.ok()) st = check_ptr(workspace, "workspace");
     if (st.ok() && x == out) st = Err(MRUN_ERR_INVALID, "out must not alias x");
-    models::Stages stages;
+    StageMarks stages;
     stages.events = (hipEvent_t *)events;
     stages.n_events = events ? n_events : 0;
     if (st.ok())
@@ -507,7 +484,7 @@ int mrun_moe_router(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t toke
     }
     if (st.ok() && lg) st = check_ptr(lg, "logits");
     if (st.ok())
-        st = tensor::router(*moe, x, tokens, lg, gates, ids, scores, nullptr, (hipStream_t)stream);
+        st = tensor::router(*moe, x, tokens, lg, gates, ids, scores, (hipStream_t)stream);
     return report(st);
 }
 

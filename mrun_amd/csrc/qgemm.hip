@@ -4,15 +4,13 @@
 //    (moe.rs:79-83, activations.rs:55-59);
 //  - dense bf16 GEMM (the router's Linear, load.rs:294-306).
 //
-// Exact affine dequant: out = sum_g [ s_g * sum_{k in g} x_k q_k + b_g * sum_{k in g} x_k ].
-// The codes 0..15 are exact in bf16, so each group's sum_k x_k q_k is an MFMA chain with f32
-// accumulation; the group's scale and bias are applied in f32 on the VALU. No bf16 rounding of
-// dequantized weights happens anywhere (q*s+b is generally not a bf16 value).
+// Affine dequant folded around the MFMA: a code q sits in the low mantissa bits of bf16 128.0
+// (0x4300 | q == 128 + q exactly), so the B tile is built with one and-or per two codes; the MFMA
+// chain over a quant group (64 k) accumulates P' = sum_k x_k (128 + q_k) in f32, and the group is
+// applied on the VALU as  acc += s * P' + (b - 128 s) * X  with X = sum_k x_k of the group. Each
+// dword of B holds codes (i, i + 4) of its word, so the A tile is staged re-paired the same way.
+// Dense B (the router's bf16 weights) goes to the MFMAs unchanged.
 //
-// Tile: 64 rows x 64 columns (per projection) x 64 k per step, 4 waves in 2 x 2, each wave one
-// 32 x 32 accumulator per projection. A rows are gathered through a row map (sorted position ->
-// token row); B codes are dequantized once per step into LDS and shared by the 4 waves. Global
-// loads of step k+1 are issued before the MFMAs of step k.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -27,13 +25,24 @@ __device__ __forceinline__ bf16x8_t lds_frag(const bf16_t *p) {
     return __builtin_bit_cast(bf16x8_t, *(const uint4 *)p);
 }
 
-// Eight 4-bit codes of one word -> eight exact bf16 (code order preserved).
-__device__ __forceinline__ uint4 codes_to_bf16(uint32_t w) {
-    uint32_t b[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) b[i] = __float_as_uint((float)((w >> (4 * i)) & 15u)) >> 16;
-    return make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16),
-                      b[6] | (b[7] << 16));
+// Eight 4-bit codes of one word -> bf16 (128 + q) pairs (q_i, q_{i+4}), i = 0..3.
+__device__ __forceinline__ uint4 codes_to_pairs(uint32_t w) {
+    return make_uint4((w & 0x000F000Fu) | 0x43004300u, ((w >> 4) & 0x000F000Fu) | 0x43004300u,
+                      ((w >> 8) & 0x000F000Fu) | 0x43004300u, ((w >> 12) & 0x000F000Fu) | 0x43004300u);
+}
+
+// Eight bf16 x_0..x_7 (one uint4) re-paired as (x_i, x_{i+4}).
+__device__ __forceinline__ uint4 pair8(const uint4 &a) {
+    return make_uint4(__builtin_amdgcn_perm(a.z, a.x, 0x05040100u),
+                      __builtin_amdgcn_perm(a.z, a.x, 0x07060302u),
+                      __builtin_amdgcn_perm(a.w, a.y, 0x05040100u),
+                      __builtin_amdgcn_perm(a.w, a.y, 0x07060302u));
+}
+
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+__device__ __forceinline__ float dot2_(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                           __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
 template <bool QUANT, bool GLU, int SUB>
@@ -47,6 +56,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
     __shared__ float Xs[SUB][BM];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (j.zero && blockIdx.x == 0 && blockIdx.y == 0)
+        for (int i = tid; i < j.n_zero; i += 256) j.zero[i] = 0;
     int e, row0, mrows;
     if (j.has_routing) {
         if (blockIdx.x >= *j.routing.n_tiles) return;
@@ -82,24 +93,22 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
     // scales: thread -> (p, sub, n)
     const bool sthread = QUANT && tid < NP * SUB * BN;
     const int sp = tid / (SUB * BN), ss = (tid / BN) % SUB, sn = tid % BN;
-    const QW &wsq = (GLU && sp) ? j.w1 : j.w0;
+    const QW &wsq = (GLU && sp == 1) ? j.w1 : j.w0;
     const size_t srow =
         ((size_t)e * wsq.out + min(n0 + sn, j.N - 1)) * (size_t)(K / wsq.group);
 
     uint4 ra0, ra1, rb0, rb1;
     uint32_t rw[WPT];
-    float rs = 0.f, rbias = 0.f;
+    uint32_t rs = 0, rbias = 0;  // raw bf16: converted when staged, a step after the load
     auto gload = [&](int k0) {
         ra0 = ((const uint4 *)(aptr + k0))[0];
         ra1 = ((const uint4 *)(aptr + k0))[1];
         if (QUANT) {
 #pragma unroll
             for (int i = 0; i < WPT; ++i) rw[i] = bcodes[(k0 >> 3) + i];
-            if (sthread) {
-                const int g = (k0 + ss * (BK / SUB)) / wsq.group;
-                rs = bf2f(wsq.scales[srow + g]);
-                rbias = wsq.biases ? bf2f(wsq.biases[srow + g]) : 0.f;
-            }
+            const int g = (k0 + ss * (BK / SUB)) / wsq.group;
+            rs = wsq.scales[srow + g];
+            rbias = wsq.biases ? (uint32_t)wsq.biases[srow + g] : 0u;
         } else {
             rb0 = ((const uint4 *)(bdense + k0))[0];
             rb1 = ((const uint4 *)(bdense + k0))[1];
@@ -118,28 +127,32 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
     for (int k0 = 0; k0 < K; k0 += BK) {
         __syncthreads();
         // stage A (and its group sums) and B into LDS
-        *(uint4 *)&As[ar * LDK + ak] = ra0;
-        *(uint4 *)&As[ar * LDK + ak + 8] = ra1;
         if (QUANT) {
+            const uint4 pa0 = pair8(ra0), pa1 = pair8(ra1);
+            *(uint4 *)&As[ar * LDK + ak] = pa0;
+            *(uint4 *)&As[ar * LDK + ak + 8] = pa1;
+            const uint32_t av[8] = {pa0.x, pa0.y, pa0.z, pa0.w, pa1.x, pa1.y, pa1.z, pa1.w};
             float xs = 0.f;
-            const uint32_t av[8] = {ra0.x, ra0.y, ra0.z, ra0.w, ra1.x, ra1.y, ra1.z, ra1.w};
 #pragma unroll
-            for (int i = 0; i < 8; ++i) xs += bf_lo(av[i]) + bf_hi(av[i]);
-            xs += __shfl_xor(xs, 1, 64);
+            for (int i = 0; i < 8; ++i) xs = dot2_(av[i], 0x3F803F80u, xs);
+            xs += dpp_f32<0xB1>(xs);  // the 4 threads of a row are one quad
             if (SUB == 1) {
-                xs += __shfl_xor(xs, 2, 64);
+                xs += dpp_f32<0x4E>(xs);
                 if ((tid & 3) == 0) Xs[0][ar] = xs;
             } else {
                 if ((tid & 1) == 0) Xs[(tid & 3) >> 1][ar] = xs;
             }
             bf16_t *bdst = &Bs[(bp * BN + bn) * LDK + bq * WPT * 8];
 #pragma unroll
-            for (int i = 0; i < WPT; ++i) *(uint4 *)(bdst + 8 * i) = codes_to_bf16(rw[i]);
+            for (int i = 0; i < WPT; ++i) *(uint4 *)(bdst + 8 * i) = codes_to_pairs(rw[i]);
             if (sthread) {
-                Sc[sp][ss][sn] = rs;
-                Bi[sp][ss][sn] = rbias;
+                const float sc = bf2f(rs);
+                Sc[sp][ss][sn] = sc;
+                Bi[sp][ss][sn] = bf2f(rbias) - 128.f * sc;
             }
         } else {
+            *(uint4 *)&As[ar * LDK + ak] = ra0;
+            *(uint4 *)&As[ar * LDK + ak + 8] = ra1;
             *(uint4 *)&Bs[bn * LDK + bq * 16] = rb0;
             *(uint4 *)&Bs[bn * LDK + bq * 16 + 8] = rb1;
         }

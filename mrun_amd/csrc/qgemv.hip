@@ -1,5 +1,5 @@
-// Decode-shaped gathered 4-bit products (gather_qmm at T <= 16, nuvec.rs:670-686) and the fused
-// down projection + combine of the MoE block (moe.rs:79-93, 161-171).
+// Decode-shaped gathered 4-bit products (gather_qmm at few rows, nuvec.rs:670-686) for the
+// facade ops and the block's generic path.
 //
 // Layout: a weight row of K codes is K/8 u32 words; LPR lanes share a row, each lane owning
 // 32-code chunks (one 128-bit load) li, li+LPR, ...; a 32-code chunk always lies in one quant
@@ -227,124 +227,6 @@ static hipError_t launch_gemv_glu(const GemvJob &j, hipStream_t stream) {
 
 hipError_t launch_gemv(const GemvJob &j, hipStream_t stream) {
     return j.glu ? launch_gemv_glu<true>(j, stream) : launch_gemv_glu<false>(j, stream);
-}
-
-// ---------------------------------------------------------------------------------------------
-// down projection + combine (decode)
-
-constexpr int kDownRows = 8;        // output rows (of D) per workgroup
-constexpr int kMaxPairs = 128;      // T*k
-constexpr int kMaxTokens = 16;
-
-template <int LPR, int CPL>
-__device__ __forceinline__ void down_rows(const QW &w, int e, const bf16_t *act, int lda,
-                                          int lo, int hi, int d0, int g, float (*yv)[kDownRows],
-                                          int li, int rsub) {
-    constexpr int RPI = 64 / LPR;
-    const int n_ch = w.in >> 5;
-    const int row = d0 + g * RPI + rsub;
-    Chunk c[CPL];
-#pragma unroll
-    for (int cc = 0; cc < CPL; ++cc) {
-        const int ch = li + cc * LPR;
-        if (ch < n_ch) c[cc] = load_chunk(w, e, row, ch);
-        else c[cc] = Chunk{make_uint4(0, 0, 0, 0), 0.f, 0.f};
-    }
-    for (int pos = lo; pos < hi; ++pos) {
-        float a = 0.f;
-#pragma unroll
-        for (int cc = 0; cc < CPL; ++cc) opaque(c[cc].q);
-#pragma unroll
-        for (int cc = 0; cc < CPL; ++cc) {
-            const int ch = li + cc * LPR;
-            if (ch < n_ch) {
-                uint4 xv[4];
-                const uint4 *src = (const uint4 *)(act + (size_t)pos * lda + ch * 32);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) xv[q] = src[q];
-                a += c[cc].s * dot32(c[cc].q, xv) + c[cc].b * sum32(xv);
-            }
-        }
-        a = group_sum<LPR>(a);
-        if (li == 0) yv[pos][g * RPI + rsub] = rbf(a);
-    }
-}
-
-template <int LPR, int CPL, int SLPR, int SCPL>
-__global__ __launch_bounds__(256) void down_combine_kernel(DownCombineJob j) {
-    constexpr int RPI = 64 / LPR, NRG = kDownRows / RPI;
-    constexpr int SRPI = 64 / SLPR, SNRG = kDownRows / SRPI;
-    __shared__ float yv[kMaxPairs][kDownRows];
-    __shared__ float ysh[kMaxTokens][kDownRows];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int d0 = blockIdx.x * kDownRows;
-    const int na = (int)*j.routing.n_active;
-    const int n_items = na * NRG;
-    for (int it = wave; it < n_items; it += 4) {
-        const int slot = it / NRG, g = it % NRG;
-        const int e = (int)j.routing.active[slot];
-        down_rows<LPR, CPL>(j.wd, e, j.act, j.wd.in, (int)j.routing.offsets[e],
-                            (int)j.routing.offsets[e + 1], d0, g, yv, lane % LPR, lane / LPR);
-    }
-    if (j.has_shared) {
-        // the shared expert's rows go to the waves after the routed items, round robin
-        for (int it = (wave - n_items % 4 + 4) % 4; it < SNRG; it += 4)
-            down_rows<SLPR, SCPL>(j.swd, 0, j.sh_act, j.swd.in, 0, j.T, d0, it, ysh, lane % SLPR,
-                                  lane / SLPR);
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < j.T * kDownRows; i += 256) {
-        const int t = i / kDownRows, dd = i % kDownRows;
-        float acc = 0.f;
-        for (int jj = 0; jj < j.k; ++jj) {
-            const int p = t * j.k + jj;
-            const int pos = (int)j.inverse[p];
-            acc += rbf(yv[pos][dd] * bf2f(j.scores[p]));
-        }
-        float r = rbf(acc);
-        if (j.has_shared) {
-            const float sg = rbf(sigmoidf_(bf2f(j.sh_logit[t])));
-            r = rbf(r + rbf(sg * ysh[t][dd]));
-        }
-        j.out[(size_t)t * j.wd.out + d0 + dd] = (bf16_t)f2bf(r);
-    }
-}
-
-template <int LPR, int CPL>
-static hipError_t launch_down_s(const DownCombineJob &j, hipStream_t stream) {
-    dim3 grid(j.wd.out / kDownRows);
-    const int sch = j.has_shared ? (j.swd.in >> 5) : 16;
-    if (sch == 16)
-        down_combine_kernel<LPR, CPL, 16, 1><<<grid, 256, 0, stream>>>(j);
-    else if (sch >= 64 && sch <= 64 * 4) {
-        const int c = (sch + 63) / 64;
-        if (c == 1) down_combine_kernel<LPR, CPL, 64, 1><<<grid, 256, 0, stream>>>(j);
-        else if (c == 2) down_combine_kernel<LPR, CPL, 64, 2><<<grid, 256, 0, stream>>>(j);
-        else if (c == 3) down_combine_kernel<LPR, CPL, 64, 3><<<grid, 256, 0, stream>>>(j);
-        else down_combine_kernel<LPR, CPL, 64, 4><<<grid, 256, 0, stream>>>(j);
-    } else if (sch >= 32) {
-        down_combine_kernel<LPR, CPL, 32, 2><<<grid, 256, 0, stream>>>(j);
-    } else if (sch >= 8) {
-        down_combine_kernel<LPR, CPL, 8, 2><<<grid, 256, 0, stream>>>(j);
-    } else {
-        return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
-}
-
-hipError_t launch_down_combine(const DownCombineJob &j, hipStream_t stream) {
-    const int n_ch = j.wd.in >> 5;
-    if (n_ch == 16) return launch_down_s<16, 1>(j, stream);
-    if (n_ch >= 64 && n_ch <= 256) {
-        const int c = (n_ch + 63) / 64;
-        if (c == 1) return launch_down_s<64, 1>(j, stream);
-        if (c == 2) return launch_down_s<64, 2>(j, stream);
-        if (c == 3) return launch_down_s<64, 3>(j, stream);
-        return launch_down_s<64, 4>(j, stream);
-    }
-    if (n_ch >= 32) return launch_down_s<32, 2>(j, stream);
-    if (n_ch >= 8) return launch_down_s<8, 2>(j, stream);
-    return hipErrorInvalidValue;
 }
 
 }  // namespace mrun

@@ -1,76 +1,13 @@
 // Router of the MoE block (moe.rs:151-159) and the stable expert permute (moe.rs:62-78):
-//  - router_gemv: bf16 logits for decode-sized token counts, one workgroup per expert row, the
-//    row read once with 128-bit loads; the accumulation order of a token does not depend on T;
 //  - topk: one wave per token — f32 softmax, bf16 gates, k rounds of a wave-wide max over
 //    (gate, id) keys, norm_topk;
 //  - permute: LDS-atomic histogram, block prefix sums, and a stable rank from per-expert token
 //    bitmaps (LDS atomicOr + popcount), so sorted rows come out in (expert, token) order.
 #include "common.hpp"
 #include "kernels.hpp"
+#include "topk.hpp"
 
 namespace mrun {
-
-// ---------------------------------------------------------------------------------------------
-// router logits (decode)
-
-template <int MAXT>
-__global__ __launch_bounds__(256) void router_gemv_kernel(const bf16_t *__restrict__ x, int T,
-                                                          int D, const bf16_t *__restrict__ W,
-                                                          const bf16_t *__restrict__ bias, int E,
-                                                          bf16_t *__restrict__ logits,
-                                                          const bf16_t *__restrict__ xw,
-                                                          bf16_t *__restrict__ xout) {
-    const int r = blockIdx.x;
-    const bf16_t *wr = (r < E) ? W + (size_t)r * D : xw;
-    float acc[MAXT];
-#pragma unroll
-    for (int t = 0; t < MAXT; ++t) acc[t] = 0.f;
-    for (int c = threadIdx.x * 8; c < D; c += 256 * 8) {
-        float wf[8];
-        unpack8(*(const uint4 *)(wr + c), wf);
-#pragma unroll
-        for (int t = 0; t < MAXT; ++t) {
-            if (t < T) {
-                float xf[8];
-                unpack8(*(const uint4 *)(x + (size_t)t * D + c), xf);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) acc[t] += xf[i] * wf[i];
-            }
-        }
-    }
-    __shared__ float red[4][MAXT];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int t = 0; t < MAXT; ++t) {
-        if (t < T) {
-            float v = group_sum<64>(acc[t]);
-            if (lane == 0) red[wave][t] = v;
-        }
-    }
-    __syncthreads();
-    if ((int)threadIdx.x < T) {
-        const int t = threadIdx.x;
-        float v = ((red[0][t] + red[1][t]) + red[2][t]) + red[3][t];
-        float l = rbf(v);
-        if (r < E) {
-            if (bias) l = rbf(l + bf2f(bias[r]));
-            logits[(size_t)t * E + r] = (bf16_t)f2bf(l);
-        } else {
-            xout[t] = (bf16_t)f2bf(l);
-        }
-    }
-}
-
-hipError_t launch_router_gemv(const bf16_t *x, int T, int D, const bf16_t *W, const bf16_t *bias,
-                              int E, bf16_t *logits, const bf16_t *xw, bf16_t *xout,
-                              hipStream_t stream) {
-    dim3 grid(E + (xw ? 1 : 0));
-    if (T <= 4)
-        router_gemv_kernel<4><<<grid, 256, 0, stream>>>(x, T, D, W, bias, E, logits, xw, xout);
-    else
-        router_gemv_kernel<16><<<grid, 256, 0, stream>>>(x, T, D, W, bias, E, logits, xw, xout);
-    return hipGetLastError();
-}
 
 // ---------------------------------------------------------------------------------------------
 // stable permute (block-wide)
@@ -221,71 +158,6 @@ hipError_t launch_permute(const uint32_t *ids, int P, int k, int E, const Permut
 // ---------------------------------------------------------------------------------------------
 // softmax + top-k (+ fused permute for decode)
 
-constexpr int kMaxExpertsPerLane = 8;  // E <= 512
-constexpr int kMaxTopK = 16;
-
-__device__ void topk_token(const bf16_t *__restrict__ lrow, int E, int k, bool norm,
-                           bf16_t *__restrict__ grow, uint32_t *__restrict__ idrow,
-                           bf16_t *__restrict__ srow) {
-    const int lane = threadIdx.x & 63;
-    float lv[kMaxExpertsPerLane];
-    uint32_t key[kMaxExpertsPerLane];
-    float m = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < kMaxExpertsPerLane; ++i) {
-        const int e = lane + 64 * i;
-        lv[i] = e < E ? bf2f(lrow[e]) : -INFINITY;
-        m = fmaxf(m, lv[i]);
-    }
-    m = wave_max(m);
-    float s = 0.f, ex[kMaxExpertsPerLane];
-#pragma unroll
-    for (int i = 0; i < kMaxExpertsPerLane; ++i) {
-        const int e = lane + 64 * i;
-        ex[i] = e < E ? expf(lv[i] - m) : 0.f;
-        s += ex[i];
-    }
-    s = group_sum<64>(s);
-#pragma unroll
-    for (int i = 0; i < kMaxExpertsPerLane; ++i) {
-        const int e = lane + 64 * i;
-        if (e < E) {
-            const uint32_t g = f2bf(ex[i] / s);
-            if (grow) grow[e] = (bf16_t)g;
-            key[i] = (g << 16) | (uint32_t)(0xffff - e);
-        } else {
-            key[i] = 0;
-        }
-    }
-    float gsel[kMaxTopK];
-#pragma unroll
-    for (int j = 0; j < kMaxTopK; ++j) {
-        if (j < k) {
-            uint32_t best = 0;
-#pragma unroll
-            for (int i = 0; i < kMaxExpertsPerLane; ++i) best = key[i] > best ? key[i] : best;
-            best = wave_max_u32(best);
-#pragma unroll
-            for (int i = 0; i < kMaxExpertsPerLane; ++i)
-                if (key[i] == best) key[i] = 0;
-            gsel[j] = bf2f(best >> 16);
-            if (lane == 0) idrow[j] = 0xffffu - (best & 0xffffu);
-        }
-    }
-    if (lane == 0) {
-        float sum = 0.f;
-        if (norm) {
-#pragma unroll
-            for (int j = 0; j < kMaxTopK; ++j)
-                if (j < k) sum += gsel[j];
-            sum = rbf(sum);
-        }
-#pragma unroll
-        for (int j = 0; j < kMaxTopK; ++j)
-            if (j < k) srow[j] = (bf16_t)f2bf(norm ? gsel[j] / sum : gsel[j]);
-    }
-}
-
 __global__ __launch_bounds__(256) void topk_kernel(const bf16_t *__restrict__ logits, int T, int E,
                                                    int k, int norm, bf16_t *__restrict__ gates,
                                                    uint32_t *__restrict__ ids,
@@ -296,34 +168,100 @@ __global__ __launch_bounds__(256) void topk_kernel(const bf16_t *__restrict__ lo
                ids + (size_t)t * k, scores + (size_t)t * k);
 }
 
-// Decode: one block of 1024 threads; wave w handles tokens w, w+16, ...; then the permute.
-__global__ __launch_bounds__(1024) void topk_permute_kernel(const bf16_t *__restrict__ logits,
-                                                            int T, int E, int k, int norm,
-                                                            bf16_t *__restrict__ gates,
-                                                            uint32_t *__restrict__ ids,
-                                                            bf16_t *__restrict__ scores,
-                                                            PermuteOut o) {
-    extern __shared__ uint32_t lds[];
-    for (int t = threadIdx.x >> 6; t < T; t += 16)
-        topk_token(logits + (size_t)t * E, E, k, norm != 0,
-                   gates ? gates + (size_t)t * E : nullptr, ids + (size_t)t * k,
-                   scores + (size_t)t * k);
-    __threadfence_block();
-    __syncthreads();
-    permute_block(ids, T * k, k, E, o, lds);
+hipError_t launch_topk(const bf16_t *logits, int T, int E, int k, bool norm, bf16_t *gates,
+                       uint32_t *ids, bf16_t *scores, hipStream_t stream) {
+    topk_kernel<<<(T + 3) / 4, 256, 0, stream>>>(logits, T, E, k, norm ? 1 : 0, gates, ids, scores);
+    return hipGetLastError();
 }
 
-hipError_t launch_topk(const bf16_t *logits, int T, int E, int k, bool norm, bf16_t *gates,
-                       uint32_t *ids, bf16_t *scores, const PermuteOut *fused,
-                       hipStream_t stream) {
-    if (fused) {
-        size_t lds = permute_lds_bytes(T, E);
-        topk_permute_kernel<<<1, 1024, lds, stream>>>(logits, T, E, k, norm ? 1 : 0, gates, ids,
-                                                      scores, *fused);
-    } else {
-        topk_kernel<<<(T + 3) / 4, 256, 0, stream>>>(logits, T, E, k, norm ? 1 : 0, gates, ids,
-                                                     scores);
+// ---------------------------------------------------------------------------------------------
+// prefill routing: top-k + ranks, then scatter
+
+constexpr int kRankTokensPerWave = 1;
+
+__global__ __launch_bounds__(256) void topk_rank_kernel(const bf16_t *__restrict__ logits, int T,
+                                                        int E, int k, int norm,
+                                                        uint32_t *__restrict__ ids,
+                                                        bf16_t *__restrict__ scores,
+                                                        uint32_t *__restrict__ counts,
+                                                        uint32_t *__restrict__ rank) {
+    constexpr int TPB = 4 * kRankTokensPerWave;
+    __shared__ uint32_t hist[512], base[512], lr[TPB * kMaxTopK];
+    const int wave = threadIdx.x >> 6;
+    const int t0 = blockIdx.x * TPB;
+    for (int e = threadIdx.x; e < E; e += 256) hist[e] = 0;
+    for (int i = 0; i < kRankTokensPerWave; ++i) {
+        const int t = t0 + wave * kRankTokensPerWave + i;
+        if (t < T)
+            topk_token(logits + (size_t)t * E, E, k, norm != 0, nullptr, ids + (size_t)t * k,
+                       scores + (size_t)t * k);
     }
+    __syncthreads();  // ids of this block are written (block-visible) and hist is clear
+    const int np = min(TPB, T - t0) * k;
+    const size_t p0 = (size_t)t0 * k;
+    if ((int)threadIdx.x < np) lr[threadIdx.x] = atomicAdd(&hist[ids[p0 + threadIdx.x]], 1u);
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += 256)
+        if (hist[e]) base[e] = atomicAdd(&counts[e], hist[e]);
+    __syncthreads();
+    if ((int)threadIdx.x < np) rank[p0 + threadIdx.x] = base[ids[p0 + threadIdx.x]] + lr[threadIdx.x];
+}
+
+hipError_t launch_topk_rank(const bf16_t *logits, int T, int E, int k, bool norm, uint32_t *ids,
+                            bf16_t *scores, uint32_t *counts, uint32_t *rank,
+                            hipStream_t stream) {
+    const int tpb = 4 * kRankTokensPerWave;
+    topk_rank_kernel<<<(T + tpb - 1) / tpb, 256, 0, stream>>>(logits, T, E, k, norm ? 1 : 0, ids,
+                                                               scores, counts, rank);
+    return hipGetLastError();
+}
+
+// Every block scans the E counts (1 KiB) itself; block 0 also writes offsets, the active list
+// and the tile list.
+__global__ __launch_bounds__(1024) void scatter_kernel(const uint32_t *__restrict__ ids,
+                                                       const uint32_t *__restrict__ rank,
+                                                       const uint32_t *__restrict__ counts, int P,
+                                                       int k, int E, PermuteOut o) {
+    __shared__ uint32_t off[1025], tmp[32];
+    const int tid = threadIdx.x;
+    const uint32_t cnt = tid < E ? counts[tid] : 0u;
+    uint32_t total;
+    const uint32_t ex = block_exclusive_scan<1024>(cnt, tmp, &total);
+    if (tid < E) off[tid] = ex;
+    __syncthreads();
+    const int p = blockIdx.x * 1024 + tid;
+    if (p < P) {
+        const uint32_t pos = off[ids[p]] + rank[p];
+        if (o.order) o.order[pos] = (uint32_t)p;
+        if (o.inverse) o.inverse[p] = pos;
+        if (o.token) o.token[pos] = (uint32_t)(p / k);
+    }
+    if (blockIdx.x != 0) return;
+    if (tid < E) o.offsets[tid] = ex;
+    if (tid == 0) o.offsets[E] = total;
+    if (o.active) {
+        uint32_t a = block_exclusive_scan<1024>(cnt > 0 ? 1u : 0u, tmp, &total);
+        if (tid < E && cnt > 0) o.active[a] = (uint32_t)tid;
+        if (tid == 0) *o.n_active = total;
+    }
+    if (o.tiles) {
+        const uint32_t m = (uint32_t)o.tile_m;
+        const uint32_t nt = (cnt + m - 1) / m;
+        const uint32_t b0 = block_exclusive_scan<1024>(nt, tmp, &total);
+        if (tid < E)
+            for (uint32_t i = 0; i < nt; ++i) {
+                uint32_t *t3 = o.tiles + 3 * (size_t)(b0 + i);
+                t3[0] = (uint32_t)tid;
+                t3[1] = ex + i * m;
+                t3[2] = min(m, cnt - i * m);
+            }
+        if (tid == 0) *o.n_tiles = total;
+    }
+}
+
+hipError_t launch_scatter(const uint32_t *ids, const uint32_t *rank, const uint32_t *counts,
+                          int P, int k, int E, const PermuteOut &out, hipStream_t stream) {
+    scatter_kernel<<<(P + 1023) / 1024, 1024, 0, stream>>>(ids, rank, counts, P, k, E, out);
     return hipGetLastError();
 }
 
