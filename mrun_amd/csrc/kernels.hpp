@@ -150,9 +150,20 @@ struct GemmJob {
     int glu;
     uint32_t *zero;  // block (0, 0) clears zero[0..n_zero) (routing counters of the next launch)
     int n_zero;
+    // a non-routed product with the same N run in the same launch (the shared expert)
+    struct {
+        const bf16_t *A;
+        int lda, M, K;
+        QW w0, w1;
+        bf16_t *out;
+        int ldo;
+    } sh;
+    int has_shared;
 };
 hipError_t launch_gemm(const GemmJob &job, hipStream_t stream);
-constexpr int kGemmTileM = 64;
+// whether launch_gemm runs the 128-row kernel (4-bit, group 64 or 128), which also takes `sh`
+bool qgemm_supported(const GemmJob &job);
+constexpr int kGemmTileM = 128;  // rows per routed tile
 constexpr int kGemmTileN = 64;
 
 // ---- elementwise ----

@@ -353,24 +353,32 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
         g.w0 = qw_of(m.switch_gate_proj), g.w1 = qw_of(m.switch_up_proj);
         g.routing = rt, g.has_routing = 1, g.max_tiles = p.max_tiles;
         g.out = act, g.ldo = I, g.glu = 1;
-        TRY_HIP(launch_gemm(g, s), "gate/up (mfma)");
-        st.mark(s);
         GemmJob dn{};
         dn.A = act, dn.lda = I, dn.a_div = 1, dn.N = D, dn.K = I;
         dn.w0 = qw_of(m.switch_down_proj), dn.routing = rt, dn.has_routing = 1;
         dn.max_tiles = p.max_tiles, dn.out = y, dn.ldo = D;
-        TRY_HIP(launch_gemm(dn, s), "down (mfma)");
-        st.mark(s);
+        GemmJob sg{}, sd{};
         if (S) {
-            GemmJob sg{};
             sg.A = x, sg.lda = D, sg.a_div = 1, sg.M = T, sg.N = S, sg.K = D;
             sg.w0 = qw_of(m.shared_gate_proj.q), sg.w1 = qw_of(m.shared_up_proj.q);
             sg.out = sh_act, sg.ldo = S, sg.glu = 1;
-            TRY_HIP(launch_gemm(sg, s), "shared gate/up (mfma)");
-            st.mark(s);
-            GemmJob sd{};
             sd.A = sh_act, sd.lda = S, sd.a_div = 1, sd.M = T, sd.N = D, sd.K = S;
             sd.w0 = qw_of(m.shared_down_proj.q), sd.out = sh_y, sd.ldo = D;
+        }
+        // the shared expert rides in the routed launches when its products have the same N
+        bool fuse = S == I && qgemm_supported(g) && qgemm_supported(dn) && qgemm_supported(sg) &&
+                    qgemm_supported(sd);
+        if (fuse) {
+            g.sh = {x, D, T, D, sg.w0, sg.w1, sh_act, S}, g.has_shared = 1;
+            dn.sh = {sh_act, S, T, S, sd.w0, QW{}, sh_y, D}, dn.has_shared = 1;
+        }
+        TRY_HIP(launch_gemm(g, s), "gate/up (mfma)");
+        st.mark(s);
+        TRY_HIP(launch_gemm(dn, s), "down (mfma)");
+        st.mark(s);
+        if (S && !fuse) {
+            TRY_HIP(launch_gemm(sg, s), "shared gate/up (mfma)");
+            st.mark(s);
             TRY_HIP(launch_gemm(sd, s), "shared down (mfma)");
             st.mark(s);
         } else {

@@ -19,7 +19,7 @@ namespace mrun {
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
 
-constexpr int BM = kGemmTileM, BN = kGemmTileN, BK = 64, LDK = BK + 8;
+constexpr int BM = 64, BN = kGemmTileN, BK = 64, LDK = BK + 8;
 
 __device__ __forceinline__ bf16x8_t lds_frag(const bf16_t *p) {
     return __builtin_bit_cast(bf16x8_t, *(const uint4 *)p);
@@ -56,15 +56,17 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
     __shared__ float Xs[SUB][BM];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (j.zero && blockIdx.x == 0 && blockIdx.y == 0)
+    if (j.zero && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0)
         for (int i = tid; i < j.n_zero; i += 256) j.zero[i] = 0;
     int e, row0, mrows;
     if (j.has_routing) {
         if (blockIdx.x >= *j.routing.n_tiles) return;
         const uint32_t *t3 = j.routing.tiles + 3 * (size_t)blockIdx.x;
         e = (int)t3[0];
-        row0 = (int)t3[1];
-        mrows = (int)t3[2];
+        row0 = (int)t3[1] + BM * (int)blockIdx.z;
+        mrows = (int)t3[2] - BM * (int)blockIdx.z;
+        if (mrows <= 0) return;
+        mrows = min(mrows, BM);
     } else {
         e = 0;
         row0 = blockIdx.x * BM;
@@ -214,10 +216,388 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Quantized grouped GEMM, group size 64: workgroup tile 128 rows x 256 B rows (glu: 128 gate + 128
+// up columns), 8 waves as 2 (rows) x 4 (columns); each wave owns 64 rows x two 32-column
+// fragments, 16 MFMAs per K step of 64.
+//  - Every global load reads whole 128-byte lines, 8 lanes to a line: A per K step, the packed
+//    codes per 4 K steps (a "super-step": 128 bytes of a B row), scales and biases per 16 K steps
+//    (a "chunk": 32 bytes of a row each). They pass through registers into LDS; A is re-paired on
+//    the way, codes stay packed (XOR-swizzled 16-byte units so fragment reads are conflict-free).
+//  - Each lane expands the 32 codes of a fragment and K step in registers. The K step's k are
+//    assigned to MFMA slots so that lane half h, sub-step s holds code word 4h + s of the step;
+//    the A tile is written in the same order (k block w at position 16 (w % 4) + 8 (w / 4)).
+//  - One barrier per K step (A, codes, scales are double-buffered); loads run 2 K steps (A),
+//    one super-step (codes) and one chunk (scales) ahead.
+//  - The VALU does one FMA per output element and K step (acc += s * P', P' the MFMA chain of the
+//    step started from zero); the affine bias  sum_k (b - 128 s) x_k = b X - 128 s X  is a small
+//    GEMM over the chunk, [rows x 6 C] x [6 C x cols], run on the MFMAs with X = sum_k x_k of a
+//    step split into three bf16 (hi + mid + lo == X exactly) against b and -128 s (exact).
+//  - A wave whose 64 rows are all past the tile only stages.
+//  - Tile t and column block nb go to workgroup L with L % 8 == t % 8: the hardware deals
+//    workgroups to the 8 XCDs round-robin, so all column blocks of a tile share one XCD's L2 and
+//    read the tile's A rows from it.
+//  - Optional shared tiles (a non-routed product of the same N, the shared expert) come first.
+
+constexpr int G_BM = 128, G_BNB = 256, G_KSC = 16, G_THREADS = 512;
+
+struct GTile {
+    const bf16_t *A;
+    int lda;
+    const uint32_t *a_map;
+    int a_div;
+    int e, row0, mrows, K;
+    const uint32_t *o_map;
+    bf16_t *out;
+    int ldo;
+};
+
+__device__ __forceinline__ uint4 expand_codes(uint32_t w, uint32_t cm, uint32_t cx) {
+    return make_uint4((w & cm) | cx, ((w >> 4) & cm) | cx, ((w >> 8) & cm) | cx,
+                      ((w >> 12) & cm) | cx);
+}
+
+// -128 s for a pair of bf16 scales (exact: a power-of-two scaling)
+__device__ __forceinline__ uint32_t neg128_pair(uint32_t w) {
+    const uint32_t lo = __float_as_uint(-128.f * bf_lo(w)) >> 16;
+    const uint32_t hi = __float_as_uint(-128.f * bf_hi(w)) & 0xFFFF0000u;
+    return lo | hi;
+}
+
+template <bool GLU>
+__global__ __launch_bounds__(G_THREADS, 1) void qgemm_kernel(GemmJob j) {
+    __shared__ __align__(16) bf16_t As[2][G_BM * LDK];          // 36 KB
+    __shared__ __align__(16) uint4 Bc[2][G_BNB * 8];            // 64 KB: codes of a super-step
+    __shared__ __align__(16) bf16_t Sb[2][2][G_BNB][G_KSC];     // 32 KB: scales, biases of a chunk
+    __shared__ __align__(16) bf16_t Xs[2][3][G_BM][G_KSC];      // 24 KB: X splits of a chunk
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (j.zero && blockIdx.x == 0)
+        for (int i = tid; i < j.n_zero; i += G_THREADS) j.zero[i] = 0;
+
+    constexpr int NCOLS = GLU ? G_BNB / 2 : G_BNB;
+    const int nblk = (j.N + NCOLS - 1) / NCOLS;
+    const int L = blockIdx.x, slot = L >> 3;
+    const int t = 8 * (slot / nblk) + (L & 7), nb = slot % nblk;
+    const int s_tiles = j.has_shared ? (j.sh.M + G_BM - 1) / G_BM : 0;
+    const bool shared_tile = t < s_tiles;
+    GTile g;
+    if (shared_tile) {
+        g.A = j.sh.A, g.lda = j.sh.lda, g.a_map = nullptr, g.a_div = 1, g.e = 0;
+        g.row0 = t * G_BM, g.mrows = min(G_BM, j.sh.M - g.row0), g.K = j.sh.K;
+        g.o_map = nullptr, g.out = j.sh.out, g.ldo = j.sh.ldo;
+    } else {
+        const int rt = t - s_tiles;
+        g.A = j.A, g.lda = j.lda, g.a_map = j.a_map, g.a_div = j.a_div;
+        g.K = j.K, g.o_map = j.o_map, g.out = j.out, g.ldo = j.ldo;
+        if (j.has_routing) {
+            if (rt >= j.max_tiles || rt >= (int)*j.routing.n_tiles) return;
+            const uint32_t *t3 = j.routing.tiles + 3 * (size_t)rt;
+            g.e = (int)t3[0], g.row0 = (int)t3[1], g.mrows = (int)t3[2];
+        } else {
+            g.e = 0, g.row0 = rt * G_BM;
+            if (g.row0 >= j.M) return;
+            g.mrows = min(G_BM, j.M - g.row0);
+        }
+    }
+    const int n0 = nb * NCOLS;
+    const int K = g.K, nks = K / BK, groups = K / 64;
+
+    // ---- staging roles
+    // A: row ar, k blocks 2q and 2q + 1 of each step
+    const int ar = tid >> 2, q = tid & 3;
+    const int apos = g.row0 + min(ar, g.mrows - 1);
+    const int arow = g.a_map ? (int)(g.a_map[apos] / (uint32_t)g.a_div) : apos;
+    const bf16_t *aptr = g.A + (size_t)arow * g.lda + 16 * q;
+    const int pw0 = 16 * ((2 * q) & 3) + 8 * ((2 * q) >> 2);
+    const int pw1 = 16 * ((2 * q + 1) & 3) + 8 * ((2 * q + 1) >> 2);
+    // weights of this tile (selected field by field: a pointer into the kernel arguments would go
+    // to scratch); under glu B rows 0..127 are gate columns, 128..255 up columns
+    const uint32_t *codes0 = shared_tile ? j.sh.w0.codes : j.w0.codes;
+    const uint32_t *codes1 = shared_tile ? (GLU ? j.sh.w1.codes : j.sh.w0.codes) : (GLU ? j.w1.codes : j.w0.codes);
+    const bf16_t *scales0 = shared_tile ? j.sh.w0.scales : j.w0.scales;
+    const bf16_t *scales1 = shared_tile ? (GLU ? j.sh.w1.scales : j.sh.w0.scales) : (GLU ? j.w1.scales : j.w0.scales);
+    const bf16_t *biases0 = shared_tile ? j.sh.w0.biases : j.w0.biases;
+    const bf16_t *biases1 = shared_tile ? (GLU ? j.sh.w1.biases : j.sh.w0.biases) : (GLU ? j.w1.biases : j.w0.biases);
+    const int wout = shared_tile ? j.sh.w0.out : j.w0.out;
+    const int wexp = shared_tile ? j.sh.w0.experts : j.w0.experts;
+    auto weight_row = [&](int r) __attribute__((always_inline)) -> uint32_t {  // B row r of the tile -> row of the weight tensors
+        const int col = min(n0 + (GLU ? (r % NCOLS) : r), j.N - 1);
+        return (uint32_t)(g.e * wout + col);
+    };
+    // codes: units u = tid + 512 i (i < 4) of a super-step: B row (tid / 8) + 64 i, 16-byte unit
+    // tid % 8; byte offsets (32-bit: the tensors stay below 4 GiB, checked by the host)
+    const uint32_t coff0 = weight_row((tid >> 3)) * (uint32_t)(K >> 1) + 16u * (tid & 7);
+    const uint32_t coff1 = weight_row((tid >> 3) + 64) * (uint32_t)(K >> 1) + 16u * (tid & 7);
+    const uint32_t coff2 = weight_row((tid >> 3) + 128) * (uint32_t)(K >> 1) + 16u * (tid & 7);
+    const uint32_t coff3 = weight_row((tid >> 3) + 192) * (uint32_t)(K >> 1) + 16u * (tid & 7);
+    const int cdst = (tid >> 3) * 8 + ((tid & 7) ^ ((tid >> 3) & 7));  // + 512 i
+    // scales (i = 0) / biases (i = 1): B row (tid / 2) % 256, 16-byte half tid % 2 of the chunk;
+    // offsets are clamped inside the tensor (a partial last chunk reads unused values)
+    const int sr = (tid >> 1) & 255;
+    const bool s_up = GLU && sr >= NCOLS;
+    const bf16_t *sbase = s_up ? scales1 : scales0, *bbase = s_up ? biases1 : biases0;
+    const uint32_t soff = weight_row(sr) * (uint32_t)groups + 8u * (tid & 1);  // in elements
+    const uint32_t slast = (uint32_t)wexp * (uint32_t)wout * (uint32_t)groups - 8u;
+    const int sdst = (sr * G_KSC + 8 * (tid & 1)) / 8;  // + 512 i, in uint4
+    struct ARegs {
+        uint4 a0, a1;
+    };
+    uint4 rc0, rc1, rc2, rc3, rs0, rs1;  // codes of the next super-step, scales/biases of the next chunk
+    auto load_a = [&](int ks, ARegs &r) __attribute__((always_inline)) {
+        const uint4 *pa = (const uint4 *)(aptr + ks * BK);
+        r.a0 = pa[0];
+        r.a1 = pa[1];
+    };
+    auto load_codes = [&](int ss) __attribute__((always_inline)) {  // super-step ss (clamped by the caller)
+        const uint32_t o = 128u * (uint32_t)ss;
+        rc0 = *(const uint4 *)((const char *)codes0 + coff0 + o);
+        rc1 = *(const uint4 *)((const char *)codes0 + coff1 + o);
+        rc2 = *(const uint4 *)((const char *)codes1 + coff2 + o);
+        rc3 = *(const uint4 *)((const char *)codes1 + coff3 + o);
+    };
+    auto load_scales = [&](int ch) __attribute__((always_inline)) {  // chunk ch (clamped by the caller)
+        const uint32_t o = min(soff + (uint32_t)(ch * G_KSC), slast);
+        rs0 = *(const uint4 *)(sbase + o);
+        rs1 = *(const uint4 *)(bbase + o);
+    };
+    auto store_codes = [&](int ss) __attribute__((always_inline)) {
+        uint4 *d = &Bc[ss & 1][cdst];
+        d[0] = rc0;
+        d[512] = rc1;
+        d[1024] = rc2;
+        d[1536] = rc3;
+    };
+    auto store_scales = [&](int ch) __attribute__((always_inline)) {
+        uint4 *d = (uint4 *)&Sb[ch & 1][0][0][0] + sdst;
+        d[0] = rs0;
+        d[512] = rs1;
+    };
+    auto stage_a = [&](const ARegs &r, int ks) __attribute__((always_inline)) {
+        const int kc = ks % G_KSC, par = (ks / G_KSC) & 1, buf = ks & 1;
+        const uint4 pa0 = pair8(r.a0), pa1 = pair8(r.a1);
+        *(uint4 *)&As[buf][ar * LDK + pw0] = pa0;
+        *(uint4 *)&As[buf][ar * LDK + pw1] = pa1;
+        float xs = 0.f;
+        xs = dot2_(pa0.x, 0x3F803F80u, xs);
+        xs = dot2_(pa0.y, 0x3F803F80u, xs);
+        xs = dot2_(pa0.z, 0x3F803F80u, xs);
+        xs = dot2_(pa0.w, 0x3F803F80u, xs);
+        xs = dot2_(pa1.x, 0x3F803F80u, xs);
+        xs = dot2_(pa1.y, 0x3F803F80u, xs);
+        xs = dot2_(pa1.z, 0x3F803F80u, xs);
+        xs = dot2_(pa1.w, 0x3F803F80u, xs);
+        xs += dpp_f32<0xB1>(xs);
+        xs += dpp_f32<0x4E>(xs);
+        // exact three-way split by truncation: hi + mid + lo == xs
+        const float hi = __uint_as_float(__float_as_uint(xs) & 0xFFFF0000u);
+        const float r1 = xs - hi;
+        const float mid = __uint_as_float(__float_as_uint(r1) & 0xFFFF0000u);
+        const float lo = r1 - mid;
+        if (q < 3) {
+            const float v = q == 0 ? hi : (q == 1 ? mid : lo);
+            Xs[par][q][ar][kc] = (bf16_t)(__float_as_uint(v) >> 16);
+        }
+        if (kc == 0 && nks - ks < G_KSC) {  // last chunk is partial: clear its unused columns
+#pragma unroll
+            for (int cc = 0; cc < G_KSC / 4; ++cc) {
+                const int c = 4 * cc + q;
+                if (c >= nks - ks) Xs[par][0][ar][c] = Xs[par][1][ar][c] = Xs[par][2][ar][c] = 0;
+            }
+        }
+    };
+
+    // ---- compute role: rows wm*64.., fragments ni at B rows bro[ni]
+    const int wm = wave >> 2, wn = wave & 3;
+    const int fr = lane & 31, fh = lane >> 5, fk = fh * 8;
+    const bool active = wm * 64 < g.mrows;
+    int bro[2];
+    bro[0] = GLU ? wn * 32 : wn * 64;
+    bro[1] = GLU ? NCOLS + wn * 32 : wn * 64 + 32;
+    const int arow0 = wm * 64 + fr;
+    uint32_t cm = 0x000F000Fu, cx = 0x43004300u;  // kept in VGPRs so and-or fuses
+    asm volatile("" : "+v"(cm), "+v"(cx));
+    f32x16_t acc[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[mi][ni][i] = 0.f;
+
+    auto compute = [&](int ks) __attribute__((always_inline)) {
+        const int kc = ks % G_KSC, buf = ks & 1, sb = (ks >> 2) & 1, par = (ks / G_KSC) & 1;
+        const bf16_t *as = As[buf];
+        uint4 cw[2];
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) {
+            const int R = bro[ni] + fr, c = 2 * (ks & 3) + fh;
+            cw[ni] = Bc[sb][R * 8 + (c ^ (R & 7))];
+        }
+        f32x16_t part[2][2];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            bf16x8_t a[2], b[2];
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) a[mi] = lds_frag(&as[(arow0 + mi * 32) * LDK + 16 * s + fk]);
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) {
+                const uint32_t w = s == 0 ? cw[ni].x : s == 1 ? cw[ni].y : s == 2 ? cw[ni].z : cw[ni].w;
+                b[ni] = __builtin_bit_cast(bf16x8_t, expand_codes(w, cm, cx));
+            }
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni) {
+                    if (s == 0) {
+                        const f32x16_t z = {};
+                        part[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mi], b[ni], z, 0, 0, 0);
+                    } else {
+                        part[mi][ni] =
+                            __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mi], b[ni], part[mi][ni], 0, 0, 0);
+                    }
+                }
+        }
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) {
+            const float sc = bf2f(Sb[par][0][bro[ni] + fr][kc]);
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[mi][ni][i] += sc * part[mi][ni][i];
+        }
+        if (kc == G_KSC - 1 || ks == nks - 1) {  // bias GEMM over the chunk's K steps
+            bf16x8_t bv[2][2];
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) {
+                const int R = bro[ni] + fr;
+                const uint4 sv = *(const uint4 *)&Sb[par][0][R][fk];
+                bv[ni][0] = lds_frag(&Sb[par][1][R][fk]);
+                bv[ni][1] = __builtin_bit_cast(
+                    bf16x8_t, make_uint4(neg128_pair(sv.x), neg128_pair(sv.y), neg128_pair(sv.z),
+                                         neg128_pair(sv.w)));
+            }
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) {
+                bf16x8_t xa[3];
+#pragma unroll
+                for (int tt = 0; tt < 3; ++tt) xa[tt] = lds_frag(&Xs[par][tt][arow0 + mi * 32][fk]);
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                    for (int u = 0; u < 2; ++u)
+#pragma unroll
+                        for (int tt = 0; tt < 3; ++tt)
+                            acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[tt], bv[ni][u],
+                                                                                  acc[mi][ni], 0, 0, 0);
+            }
+        }
+    };
+
+    // ---- pipeline (nks is a multiple of 4)
+    const int nss = nks / 4, nch = (nks + G_KSC - 1) / G_KSC;
+    ARegs ra0, ra1;
+    load_codes(0);
+    load_scales(0);
+    load_a(0, ra0);
+    load_a(1, ra1);
+    store_codes(0);
+    store_scales(0);
+    load_codes(min(1, nss - 1));
+    load_scales(min(1, nch - 1));
+    stage_a(ra0, 0);
+    load_a(2, ra0);
+    __syncthreads();
+    // K step k: compute k, stage k + 1 from `next` (loaded two steps ago), refill `next` with k + 3
+    auto step = [&](int k, bool super_end, ARegs &next) __attribute__((always_inline)) {
+        if (active) compute(k);
+        if (k + 1 < nks) {
+            if (super_end) {  // next super-step: its codes were loaded one super-step ago
+                store_codes((k + 1) >> 2);
+                load_codes(min(((k + 1) >> 2) + 1, nss - 1));
+                if ((k + 1) % G_KSC == 0) {
+                    store_scales((k + 1) / G_KSC);
+                    load_scales(min((k + 1) / G_KSC + 1, nch - 1));
+                }
+            }
+            stage_a(next, k + 1);
+        }
+        load_a(min(k + 3, nks - 1), next);
+        __syncthreads();
+    };
+    for (int ks = 0; ks < nks; ks += 4) {
+        step(ks, false, ra1);
+        step(ks + 1, false, ra0);
+        step(ks + 2, false, ra1);
+        step(ks + 3, true, ra0);
+    }
+    if (!active) return;
+
+    // epilogue: glu -> R(silu(R(gate)) * R(up)); else R(.) (+ bias: R(R(.) + b))
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) {
+        if (GLU) {
+            const int col = n0 + wn * 32 + fr;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int r = wm * 64 + mi * 32 + 8 * (i >> 2) + 4 * fh + (i & 3);
+                if (r < g.mrows && col < j.N) {
+                    const int pos = g.row0 + r;
+                    const int orow = g.o_map ? (int)g.o_map[pos] : pos;
+                    const float gt = rbf(acc[mi][0][i]), u = rbf(acc[mi][1][i]);
+                    g.out[(size_t)orow * g.ldo + col] = (bf16_t)f2bf((gt * sigmoidf_(gt)) * u);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) {
+                const int col = n0 + wn * 64 + ni * 32 + fr;
+                const float bias = (j.bias && col < j.N) ? bf2f(j.bias[col]) : 0.f;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int r = wm * 64 + mi * 32 + 8 * (i >> 2) + 4 * fh + (i & 3);
+                    if (r < g.mrows && col < j.N) {
+                        const int pos = g.row0 + r;
+                        const int orow = g.o_map ? (int)g.o_map[pos] : pos;
+                        float v = acc[mi][ni][i];
+                        if (j.bias) v = rbf(v) + bias;
+                        g.out[(size_t)orow * g.ldo + col] = (bf16_t)f2bf(v);
+                    }
+                }
+            }
+        }
+    }
+}
+
+bool qgemm_supported(const GemmJob &j) {
+    auto ok = [](const QW &w, int K) {
+        // 16-byte units of codes and of scales per row; 32-bit byte offsets into the codes
+        return w.codes && w.scales && w.biases && w.bits == 4 && w.group == 64 && K % 512 == 0 &&
+               (size_t)w.experts * w.out * (size_t)(K / 2) < ((size_t)1 << 32);
+    };
+    if (j.bd || !ok(j.w0, j.K) || (j.glu && !ok(j.w1, j.K))) return false;
+    if (j.has_shared && (!ok(j.sh.w0, j.sh.K) || (j.glu && !ok(j.sh.w1, j.sh.K)))) return false;
+    return true;
+}
+
 hipError_t launch_gemm(const GemmJob &j, hipStream_t stream) {
+    if (qgemm_supported(j)) {
+        const int ncols = j.glu ? G_BNB / 2 : G_BNB;
+        const int nblk = (j.N + ncols - 1) / ncols;
+        const int s_tiles = j.has_shared ? (j.sh.M + G_BM - 1) / G_BM : 0;
+        const int r_tiles = j.has_routing ? j.max_tiles : (j.M + G_BM - 1) / G_BM;
+        const int tiles8 = (s_tiles + r_tiles + 7) / 8 * 8;
+        if (tiles8 == 0) return hipSuccess;
+        const dim3 grid(tiles8 * nblk);
+        if (j.glu) qgemm_kernel<true><<<grid, G_THREADS, 0, stream>>>(j);
+        else qgemm_kernel<false><<<grid, G_THREADS, 0, stream>>>(j);
+        return hipGetLastError();
+    }
+    if (j.has_shared) return hipErrorInvalidValue;  // only the kernel above takes shared tiles
+    // routed tiles hold up to kGemmTileM rows: grid.z walks them in steps of BM
     const int tiles = j.has_routing ? j.max_tiles : (j.M + BM - 1) / BM;
     if (tiles <= 0) return hipSuccess;
-    dim3 grid(tiles, (j.N + BN - 1) / BN);
+    dim3 grid(tiles, (j.N + BN - 1) / BN, j.has_routing ? kGemmTileM / BM : 1);
     if (!j.bd) {
         const bool sub2 = j.w0.group == 32;
         if (j.glu) {
