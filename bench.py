@@ -188,7 +188,18 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only copy MIB MiB device to device 10 times (the byte counters' reference)")
     args = ap.parse_args(argv)
+    if args.calibrate_copy:
+        import torch
+        src = torch.empty(args.calibrate_copy << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"[bench] copied {args.calibrate_copy} MiB x 10", file=sys.stderr)
+        return 0
     if args.gpus != 1:
         print("bench.py measures one GPU: the MoE block runs on a single MI355X in this build "
               "(expert-parallel sharding is described in DESIGN.md, not implemented)",
