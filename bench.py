@@ -60,15 +60,18 @@ def proj_bytes(out: int, in_: int, group: int = 64) -> int:
 
 
 def decode_bytes(shape, n_active: int, T: int) -> dict:
-    """Algorithmic HBM bytes per stage and per block at decode."""
+    """Algorithmic HBM bytes of each decode launch and of the block.
+
+    router: router rows and the shared gate row; gate_up: the active experts' and the shared
+    expert's gate/up rows, activations in, act out; down_combine: the down rows, act in, out."""
     D, E, I, S = shape.hidden, shape.experts, shape.intermediate, shape.shared
     k = shape.top_k
     P = T * k
-    gu = (n_active * 2 * proj_bytes(I, D) + (2 * proj_bytes(S, D) if S else 0)
-          + 2 * T * D + 2 * (P * I + T * S))
-    dn = (n_active * proj_bytes(D, I) + (proj_bytes(D, S) if S else 0)
-          + 2 * (P * I + T * S) + 2 * T * D + 2 * P + 4 * P)
     router = 2 * E * D + (2 * D if S else 0) + 2 * T * D + 2 * T * (E + 1)
+    gu = (n_active * 2 * proj_bytes(I, D) + (2 * proj_bytes(S, D) if S else 0)
+          + 2 * T * D + 2 * (P * I + T * S) + 2 * T * E)
+    dn = (n_active * proj_bytes(D, I) + (proj_bytes(D, S) if S else 0)
+          + 2 * (P * I + T * S) + 2 * T * D + 2 * P + 4 * P + 2 * T)
     block = (n_active * 3 * proj_bytes(I, D) + (3 * proj_bytes(S, D) if S else 0)
              + 2 * E * D + (2 * D if S else 0) + 4 * D * T)
     return {"gate_up": gu, "down_combine": dn, "router": router, "block": block}
@@ -237,7 +240,7 @@ def main(argv=None) -> int:
     main_pt, x_main = decode_point(args.tokens, args.steps, args.warmup)
     gu_us = main_pt["stages_us"]["gate_up"]
     achieved = main_pt["bytes"]["gate_up"] / (gu_us * 1e-6)
-    roofline = {"kernel": "gemv_kernel (routed + shared gate/up, SwiGLU fused)", "bound": "hbm",
+    roofline = {"kernel": "decode_gateup_kernel (routed + shared gate/up, SwiGLU fused)", "bound": "hbm",
                 "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                 "frac": achieved / HBM_PEAK, "traffic": None,
                 "bytes_per_launch": main_pt["bytes"]["gate_up"], "us_per_launch": gu_us}

@@ -1,13 +1,16 @@
 // Decode schedule of the MoE block (T <= 16 tokens, T*k <= 128 pairs): three launches, no global
 // routing round trip and no permutation (SparseMoe::forward, moe.rs:149-174).
 //
-//   K1 router  : router logits (+ bias), the shared expert's gate logit and its gate/up + SwiGLU.
-//                The shared expert does not depend on the routing, so it runs beside the router.
-//   K2 gate/up : every workgroup re-derives the top-k of all T tokens from the L2-resident logits
-//                (the same code as the router op, so the same bits), picks the slot-th active expert
-//                (experts in ascending order), and streams that expert's gate/up rows for its pairs.
-//   K3 down    : prefetches the shared expert's down rows, re-derives top-k and scores, computes the
-//                routed down rows of every active expert for its 8 output rows, then the combine:
+//   K1 router  : router logits (+ bias) and the shared expert's gate logit, one wave per row.
+//   K2 gate/up : the shared expert's gate/up + SwiGLU (it does not depend on the routing, so those
+//                workgroups stream from the first cycle), and the routed experts: every routed
+//                workgroup re-derives the top-k of all T tokens from the logits (the same code as
+//                the router op, so the same bits; T > 4 reads them from a top-k launch instead),
+//                picks the slot-th active expert (experts in ascending order) and streams that
+//                expert's gate/up rows for its pairs. The first routed workgroup publishes the
+//                routing for K3.
+//   K3 down    : prefetches the shared expert's down rows, reads the routing, computes the routed
+//                down rows of every active expert for its 8 output rows, then the combine:
 //                out = R(R(sum_j R(y[t,j] * s[t,j])) + R(R(sigmoid(g_t)) * shared[t])).
 // Pair p = t*k + j indexes the activations (act [T*k, I]), so no argsort is needed at decode; the
 // results are the same as the sorted dispatch's, row by row.
@@ -18,7 +21,7 @@
 
 namespace mrun {
 
-constexpr int kMaxT = 16, kMaxP = 128, kDownRowsPerWG = 8;
+constexpr int kMaxT = 16, kMaxP = 128;
 
 // Rows [row_base + g*RPI + rsub] of w0 (and w1 with glu), g < RG, for the pairs set in pm0|pm1
 // (bit p: pair p reads A row p / a_div and writes output row p). The next pair's activations are
@@ -157,40 +160,29 @@ hipError_t launch_rows(const bf16_t *x, int T, int D, const bf16_t *W, const bf1
 }
 
 // ---------------------------------------------------------------------------------------------
-// K1: router + shared gate logit + shared gate/up
+// K1: router logits + the shared expert's gate logit
 
-template <int MAXT, int LPR, int CPL>
+template <int MAXT>
 __global__ __launch_bounds__(256) void decode_router_kernel(DecodeJob j) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int n_rows = j.E + (j.S ? 1 : 0);
-    const int n_rb = (n_rows + 3) / 4;
-    if ((int)blockIdx.x < n_rb) {
-        const int r = blockIdx.x * 4 + wave;
-        if (r < j.E)
-            router_row<MAXT>(j.x, j.T, j.D, j.router + (size_t)r * j.D,
-                             j.router_bias ? j.router_bias + r : nullptr, j.logits + r, j.E, lane);
-        else if (r == j.E)
-            router_row<MAXT>(j.x, j.T, j.D, j.sh_gate_w, j.sh_gate_b, j.sh_logit, 1, lane);
-        return;
-    }
-    // shared expert gate/up: 16 rows x up to 4 tokens per workgroup
-    constexpr int RPI = 64 / LPR, RG = 4;
-    const int sb = blockIdx.x - n_rb, n_row_blocks = j.S / 16;
-    const int rb = sb % n_row_blocks, t0 = (sb / n_row_blocks) * 4;
-    const int tn = min(4, j.T - t0);
-    const uint64_t toks = ((1ull << tn) - 1) << t0;
-    gemv_wave<LPR, CPL, RG, true>(j.sg, j.su, 0, (rb * 4 + wave) * RG * RPI, j.x, j.D, 1, toks, 0,
-                                  j.sh_act, j.S, lane);
+    const int r = blockIdx.x * 4 + wave;
+    if (r < j.E)
+        router_row<MAXT>(j.x, j.T, j.D, j.router + (size_t)r * j.D,
+                         j.router_bias ? j.router_bias + r : nullptr, j.logits + r, j.E, lane);
+    else if (r == j.E && j.S)
+        router_row<MAXT>(j.x, j.T, j.D, j.sh_gate_w, j.sh_gate_b, j.sh_logit, 1, lane);
 }
 
 // ---------------------------------------------------------------------------------------------
 // shared by K2 and K3: the top-k of every token into LDS, and the active-expert mask
 
-__device__ __forceinline__ void all_topk(const DecodeJob &j, uint32_t *sid, bf16_t *ssc,
-                                         uint32_t *mask) {
-    const int wave = threadIdx.x >> 6;
+__device__ __forceinline__ void all_topk(const DecodeJob &j, bool compute, uint32_t *sid,
+                                         bf16_t *ssc, uint32_t *mask) {
+    // token t goes to wave (t + blockIdx.x) % 4: the workgroups sharing a CU spread their top-k
+    // over its four SIMDs
+    const int wave = (int)((threadIdx.x >> 6) + 4 - (blockIdx.x & 3)) & 3;
     if (threadIdx.x < 16) mask[threadIdx.x] = 0;
-    if (j.topk_in_kernel) {
+    if (compute) {
         for (int t = wave; t < j.T; t += 4)
             topk_token(j.logits + (size_t)t * j.E, j.E, j.k, j.norm != 0, nullptr, sid + t * j.k,
                        ssc + t * j.k);
@@ -214,74 +206,147 @@ __device__ __forceinline__ void pairs_of(const uint32_t *sid, int P, int e, int 
 }
 
 // ---------------------------------------------------------------------------------------------
-// K2: routed gate/up
+// K2: shared + routed gate/up
 
-template <int LPR, int CPL>
+// K2 workgroups: 4 waves x RG rows of one projection pair each, up to 4 tokens for the shared
+// expert. Few rows per wave keep several waves per SIMD, so their dependent reductions overlap.
+__host__ __device__ inline int shared_gateup_blocks(const DecodeJob &j, int rg) {
+    return j.S ? (j.S / (4 * rg)) * ((j.T + 3) / 4) : 0;
+}
+
+template <int LPR, int CPL, int RG>
 __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeJob j) {
     __shared__ uint32_t sid[kMaxP], mask[16];
     __shared__ bf16_t ssc[kMaxP];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    all_topk(j, sid, ssc, mask);
-    // the slot-th active expert, experts in ascending order
-    const int slot = blockIdx.y;
-    int e = -1, n = 0;
-    for (int w = 0; w < (j.E + 31) / 32; ++w) {
-        const uint32_t mw = mask[w];
-        const int c = __popc(mw);
-        if (e < 0 && slot < n + c) {
-            uint32_t m = mw;
-            for (int i = 0; i < slot - n; ++i) m &= m - 1;
-            e = w * 32 + __ffs(m) - 1;
-        }
-        n += c;
-    }
-    if (e < 0) return;
+    constexpr int RPI = 64 / LPR;
+    const int n_sh = shared_gateup_blocks(j, RG * RPI);
+    // one gemv_wave call for both kinds of workgroup (its code is large): pick its operands
+    const bool sh = (int)blockIdx.x < n_sh;
+    auto pick = [&](const QW &a, const QW &b) {  // field by field: no copy of the arguments
+        QW q;
+        q.codes = sh ? a.codes : b.codes;
+        q.scales = sh ? a.scales : b.scales;
+        q.biases = sh ? a.biases : b.biases;
+        q.experts = sh ? a.experts : b.experts;
+        q.out = sh ? a.out : b.out;
+        q.in = sh ? a.in : b.in;
+        q.group = sh ? a.group : b.group;
+        q.bits = sh ? a.bits : b.bits;
+        return q;
+    };
+    const QW w0 = pick(j.sg, j.wg), w1 = pick(j.su, j.wu);
+    int e = 0, row_base, a_div, ldo;
     uint64_t pm0, pm1;
-    pairs_of(sid, j.T * j.k, e, lane, pm0, pm1);
-    constexpr int RPI = 64 / LPR, RG = 4;
-    gemv_wave<LPR, CPL, RG, true>(j.wg, j.wu, e, (blockIdx.x * 4 + wave) * RG * RPI, j.x, j.D, j.k,
-                                  pm0, pm1, j.act, j.I, lane);
+    bf16_t *out;
+    if (sh) {  // shared expert gate/up: 4 * RG * RPI rows x up to 4 tokens
+        const int n_row_blocks = j.S / (4 * RG * RPI);
+        const int rb = blockIdx.x % n_row_blocks, t0 = (blockIdx.x / n_row_blocks) * 4;
+        const int tn = min(4, j.T - t0);
+        row_base = (rb * 4 + wave) * RG * RPI, a_div = 1, ldo = j.S, out = j.sh_act;
+        pm0 = ((1ull << tn) - 1) << t0, pm1 = 0;
+    } else {
+        const int r = blockIdx.x - n_sh, row_blocks = j.I / (4 * RG * RPI);
+        const int slot = r / row_blocks, rb = r % row_blocks;
+        all_topk(j, j.topk_in_kernel != 0, sid, ssc, mask);
+        if (r == 0 && j.topk_in_kernel) {  // publish the routing for K3
+            const int P = j.T * j.k;
+            if ((int)threadIdx.x < P) {
+                j.ids[threadIdx.x] = sid[threadIdx.x];
+                j.scores[threadIdx.x] = ssc[threadIdx.x];
+            }
+        }
+        // the slot-th active expert, experts in ascending order
+        e = -1;
+        int n = 0;
+        for (int w = 0; w < (j.E + 31) / 32; ++w) {
+            const uint32_t mw = mask[w];
+            const int c = __popc(mw);
+            if (e < 0 && slot < n + c) {
+                uint32_t m = mw;
+                for (int i = 0; i < slot - n; ++i) m &= m - 1;
+                e = w * 32 + __ffs(m) - 1;
+            }
+            n += c;
+        }
+        if (e < 0) return;
+        pairs_of(sid, j.T * j.k, e, lane, pm0, pm1);
+        row_base = (rb * 4 + wave) * RG * RPI, a_div = j.k, ldo = j.I, out = j.act;
+    }
+    gemv_wave<LPR, CPL, RG, true>(w0, w1, e, row_base, j.x, j.D, a_div, pm0, pm1, out, ldo, lane);
 }
 
 // ---------------------------------------------------------------------------------------------
 // K3: down + combine
 
-template <int LPR, int CPL, int SLPR, int SCPL, int PB>
+template <int LPR, int CPL, int SLPR, int SCPL, int PB, int kDownRowsPerWG>
 __global__ __launch_bounds__(256) void decode_down_kernel(DecodeJob j) {
     constexpr int RPI = 64 / LPR, NRG = kDownRowsPerWG / RPI;
     constexpr int SRPI = 64 / SLPR, SNRG = kDownRowsPerWG / SRPI, SG = (SNRG + 3) / 4;
-    __shared__ uint32_t sid[kMaxP], mask[16];
+    __shared__ uint32_t sid[kMaxP];
     __shared__ bf16_t ssc[kMaxP];
     __shared__ float yv[kMaxP][kDownRowsPerWG];
     __shared__ float ysh[kMaxT][kDownRowsPerWG];
+    __shared__ bf16_t shl[kMaxT];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int d0 = blockIdx.x * kDownRowsPerWG;
 
-    // the shared expert's rows do not depend on the routing: start their loads first
+    // the routing is loaded first (loads complete in issue order), then what does not depend on
+    // it: the shared expert's rows and first activation row, the shared gate logits, this wave's
+    // first activation rows
+    const int P = j.T * j.k;
+    const uint32_t my_id = j.ids[min((int)threadIdx.x, P - 1)];
+    const uint32_t my_sc = j.scores[min((int)threadIdx.x, P - 1)];
     WRow<SCPL> sr[SG];
-    if (j.S) {
+    const int sli = lane % SLPR;
+    XRaw scur[SCPL];
+    {
+        // unconditional: without a shared expert the routed down weights and activations stand in
+        // (never used), so no load sits under a condition
+        const bool has_s = j.S != 0;
+        QW sd;
+        sd.codes = has_s ? j.sd.codes : j.wd.codes;
+        sd.scales = has_s ? j.sd.scales : j.wd.scales;
+        sd.biases = has_s ? j.sd.biases : j.wd.biases;
+        sd.experts = has_s ? j.sd.experts : j.wd.experts;
+        sd.out = has_s ? j.sd.out : j.wd.out;
+        sd.in = has_s ? j.sd.in : j.wd.in;
+        sd.group = has_s ? j.sd.group : j.wd.group;
+        sd.bits = has_s ? j.sd.bits : j.wd.bits;
 #pragma unroll
         for (int i = 0; i < SG; ++i) {
             const int g = wave + 4 * i;
-            load_wrow<SCPL>(j.sd, 0, g < SNRG ? d0 + g * SRPI + lane / SLPR : j.D, lane % SLPR,
-                            SLPR, sr[i]);
+            load_wrow<SCPL>(sd, 0, g < SNRG ? d0 + g * SRPI + lane / SLPR : j.D, sli, SLPR, sr[i]);
         }
+        load_xrow_raw<SCPL>(has_s ? j.sh_act : j.act, sli, SLPR, (has_s ? j.S : j.I) >> 5, scur);
     }
-    all_topk(j, sid, ssc, mask);
+    // clamped indices and unconditional LDS writes (threads past the end repeat the last value):
+    // a load used under a condition would make the wait there cover every load issued before
+    const bf16_t *shl_src = j.S ? j.sh_logit : j.scores;  // any valid pointer without a shared expert
+    const uint32_t my_shl = shl_src[min((int)threadIdx.x, j.T - 1)];
+    const int li = lane % LPR, rsub = lane / LPR;
+    const int per_wave = (P + 3) / 4;
+    const int p_lo = wave * per_wave, p_hi = min(P, p_lo + per_wave);
+    XRaw xr[PB][CPL];
+    auto load_act = [&](int pb) {  // rows clamped into [0, P): also a wave without pairs loads
+#pragma unroll
+        for (int b = 0; b < PB; ++b)
+            load_xrow_raw<CPL>(j.act + (size_t)max(0, min(pb + b, p_hi - 1)) * j.I, li, LPR,
+                               j.I >> 5, xr[b]);
+    };
+    load_act(p_lo);
+    sid[min((int)threadIdx.x, P - 1)] = my_id;
+    ssc[min((int)threadIdx.x, P - 1)] = (bf16_t)my_sc;
+    __syncthreads();
 
     // work: for each pair p (expert sid[p]) its NRG row groups of this workgroup's rows; a wave
     // takes PB pairs at a time and issues all their loads before computing
-    const int P = j.T * j.k, li = lane % LPR, rsub = lane / LPR;
-    const int per_wave = (P + 3) / 4;
-    const int p_lo = wave * per_wave, p_hi = min(P, p_lo + per_wave);
     for (int pb = p_lo; pb < p_hi; pb += PB) {
-        XRaw xr[PB][CPL];
+        if (pb != p_lo) load_act(pb);
         WRow<CPL> wr[PB][NRG];
 #pragma unroll
         for (int b = 0; b < PB; ++b) {
-            const int p = min(pb + b, p_hi - 1);
-            const int e = (int)sid[p];
-            load_xrow_raw<CPL>(j.act + (size_t)p * j.I, li, LPR, j.I >> 5, xr[b]);
+            const int e = (int)sid[min(pb + b, p_hi - 1)];
 #pragma unroll
             for (int g = 0; g < NRG; ++g)
                 load_wrow<CPL>(j.wd, e, d0 + g * RPI + rsub, li, LPR, wr[b][g]);
@@ -300,16 +365,14 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeJob j) {
         }
     }
     if (j.S) {
-        const int sli = lane % SLPR;
-        XRaw cur[SCPL], nxt[SCPL];
-        load_xrow_raw<SCPL>(j.sh_act, sli, SLPR, j.S >> 5, cur);
+        XRaw nxt[SCPL];
         for (int t = 0; t < j.T; ++t) {
             load_xrow_raw<SCPL>(j.sh_act + (size_t)min(t + 1, j.T - 1) * j.S, sli, SLPR, j.S >> 5,
                                 nxt);
             XChunk xc[SCPL];
-            pair_xrow<SCPL>(cur, xc);
+            pair_xrow<SCPL>(scur, xc);
 #pragma unroll
-            for (int c = 0; c < SCPL; ++c) cur[c] = nxt[c];
+            for (int c = 0; c < SCPL; ++c) scur[c] = nxt[c];
 #pragma unroll
             for (int i = 0; i < SG; ++i) {
                 const int g = wave + 4 * i;
@@ -319,6 +382,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeJob j) {
             }
         }
     }
+    shl[min((int)threadIdx.x, kMaxT - 1)] = (bf16_t)my_shl;
     __syncthreads();
     for (int i = threadIdx.x; i < j.T * kDownRowsPerWG; i += 256) {
         const int t = i / kDownRowsPerWG, dd = i % kDownRowsPerWG;
@@ -329,7 +393,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeJob j) {
         }
         float r = rbf(acc);
         if (j.S) {
-            const float sg = rbf(sigmoidf_(bf2f(j.sh_logit[t])));
+            const float sg = rbf(sigmoidf_(bf2f(shl[t])));
             r = rbf(r + rbf(sg * ysh[t][dd]));
         }
         j.out[(size_t)t * j.D + d0 + dd] = (bf16_t)f2bf(r);
@@ -340,36 +404,30 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeJob j) {
 
 template <int MAXT>
 static void launch_k1(const DecodeJob &j, hipStream_t s) {
-    const int n_rb = (j.E + (j.S ? 1 : 0) + 3) / 4;
-    // LPR 64 (D >= 2048): 16 rows x 4 tokens per workgroup
-    const int sh_blocks = j.S ? (j.S / 16) * ((j.T + 3) / 4) : 0;
-    const int n_ch = j.D >> 5;
-    dim3 grid(n_rb + sh_blocks);
-    if (n_ch <= 64) decode_router_kernel<MAXT, 64, 1><<<grid, 256, 0, s>>>(j);
-    else if (n_ch <= 128) decode_router_kernel<MAXT, 64, 2><<<grid, 256, 0, s>>>(j);
-    else if (n_ch <= 192) decode_router_kernel<MAXT, 64, 3><<<grid, 256, 0, s>>>(j);
-    else decode_router_kernel<MAXT, 64, 4><<<grid, 256, 0, s>>>(j);
+    dim3 grid((j.E + (j.S ? 1 : 0) + 3) / 4);
+    decode_router_kernel<MAXT><<<grid, 256, 0, s>>>(j);
 }
 
 template <int LPR, int CPL>
 static void launch_k3_s(const DecodeJob &j, hipStream_t s) {
-    // pairs per load batch: keep a batch's activations and weight rows within ~128 registers
-    constexpr int NRG = kDownRowsPerWG / (64 / LPR);
+    // 4 output rows per workgroup; pairs per load batch keep a batch's activations and weight rows
+    // within ~128 registers
+    constexpr int DR = 4;
+    constexpr int NRG = DR / (64 / LPR) > 0 ? DR / (64 / LPR) : 1;
     constexpr int PB = (NRG * CPL <= 2) ? 4 : (NRG * CPL <= 4 ? 2 : 1);
-    dim3 grid(j.D / kDownRowsPerWG);
+    dim3 grid(j.D / DR);
     const int sch = j.S ? j.S >> 5 : 16;
-    if (sch == 16) decode_down_kernel<LPR, CPL, 16, 1, PB><<<grid, 256, 0, s>>>(j);
-    else if (sch < 64) decode_down_kernel<LPR, CPL, 32, 2, PB><<<grid, 256, 0, s>>>(j);
-    else if (sch <= 64) decode_down_kernel<LPR, CPL, 64, 1, PB><<<grid, 256, 0, s>>>(j);
-    else if (sch <= 128) decode_down_kernel<LPR, CPL, 64, 2, PB><<<grid, 256, 0, s>>>(j);
-    else decode_down_kernel<LPR, CPL, 64, 4, PB><<<grid, 256, 0, s>>>(j);
+    if (sch == 16) decode_down_kernel<LPR, CPL, 16, 1, PB, DR><<<grid, 256, 0, s>>>(j);
+    else if (sch < 64) decode_down_kernel<LPR, CPL, 32, 2, PB, DR><<<grid, 256, 0, s>>>(j);
+    else if (sch <= 64) decode_down_kernel<LPR, CPL, 64, 1, PB, DR><<<grid, 256, 0, s>>>(j);
+    else if (sch <= 128) decode_down_kernel<LPR, CPL, 64, 2, PB, DR><<<grid, 256, 0, s>>>(j);
+    else decode_down_kernel<LPR, CPL, 64, 4, PB, DR><<<grid, 256, 0, s>>>(j);
 }
 
 bool decode_supported(int D, int I, int S, int T, int k, int E) {
     auto ok = [](int K) { return K >= 512 && K <= 8192 && K % 32 == 0; };
     return T >= 1 && T <= kMaxT && T * k <= kMaxP && E <= 512 && ok(D) && ok(I) &&
-           (S == 0 || (ok(S) && S % 16 == 0)) && D % kDownRowsPerWG == 0 && I % 16 == 0 &&
-           D >= 2048;
+           (S == 0 || (ok(S) && S % 16 == 0)) && D % 4 == 0 && I % 16 == 0 && D >= 2048;
 }
 
 hipError_t launch_decode(const DecodeJob &j, hipStream_t s, StageMarks *marks) {
@@ -384,11 +442,25 @@ hipError_t launch_decode(const DecodeJob &j, hipStream_t s, StageMarks *marks) {
     if (marks) marks->mark(s);
 
     const int n_ch = j.D >> 5;
-    dim3 g2(j.I / 16, j.max_slots);
-    if (n_ch <= 64) decode_gateup_kernel<64, 1><<<g2, 256, 0, s>>>(j);
-    else if (n_ch <= 128) decode_gateup_kernel<64, 2><<<g2, 256, 0, s>>>(j);
-    else if (n_ch <= 192) decode_gateup_kernel<64, 3><<<g2, 256, 0, s>>>(j);
-    else decode_gateup_kernel<64, 4><<<g2, 256, 0, s>>>(j);
+    // rows per wave: about 1024 routed workgroups at T = 1, 2 and 4 (8, 16, 32 expert slots)
+    const int rg = j.T == 1 ? 1 : (j.T == 2 ? 2 : 4);
+    dim3 g2(shared_gateup_blocks(j, rg) + (j.I / (4 * rg)) * j.max_slots);
+    if (rg == 1) {
+        if (n_ch <= 64) decode_gateup_kernel<64, 1, 1><<<g2, 256, 0, s>>>(j);
+        else if (n_ch <= 128) decode_gateup_kernel<64, 2, 1><<<g2, 256, 0, s>>>(j);
+        else if (n_ch <= 192) decode_gateup_kernel<64, 3, 1><<<g2, 256, 0, s>>>(j);
+        else decode_gateup_kernel<64, 4, 1><<<g2, 256, 0, s>>>(j);
+    } else if (rg == 2) {
+        if (n_ch <= 64) decode_gateup_kernel<64, 1, 2><<<g2, 256, 0, s>>>(j);
+        else if (n_ch <= 128) decode_gateup_kernel<64, 2, 2><<<g2, 256, 0, s>>>(j);
+        else if (n_ch <= 192) decode_gateup_kernel<64, 3, 2><<<g2, 256, 0, s>>>(j);
+        else decode_gateup_kernel<64, 4, 2><<<g2, 256, 0, s>>>(j);
+    } else {
+        if (n_ch <= 64) decode_gateup_kernel<64, 1, 4><<<g2, 256, 0, s>>>(j);
+        else if (n_ch <= 128) decode_gateup_kernel<64, 2, 4><<<g2, 256, 0, s>>>(j);
+        else if (n_ch <= 192) decode_gateup_kernel<64, 3, 4><<<g2, 256, 0, s>>>(j);
+        else decode_gateup_kernel<64, 4, 4><<<g2, 256, 0, s>>>(j);
+    }
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (marks) marks->mark(s);

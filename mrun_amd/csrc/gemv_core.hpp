@@ -70,7 +70,8 @@ __device__ __forceinline__ float dot_chunk(const uint4 &q, const XChunk &x) {
 
 // One weight row's chunks for one lane: codes and the raw bf16 scale and bias. Loads use clamped
 // addresses and are never followed by a use inside a condition, so all of a wave's loads are in
-// flight together; `ok` masks the chunks that lie past the row or the matrix.
+// flight together; `ok` bit c masks the chunks that lie past the row or the matrix, bit 31 says
+// whether the weight has biases.
 template <int CPL>
 struct WRow {
     uint4 q[CPL];
@@ -85,7 +86,9 @@ __device__ __forceinline__ void load_wrow(const QW &w, int e, int row, int li, i
     const int groups = w.in / w.group;
     const size_t rr = (size_t)e * w.out + min(row, w.out - 1);
     const uint32_t *codes = w.codes + rr * (size_t)(w.in >> 3);
-    r.ok = 0;
+    // without biases the scales stand in, so the load is unconditional; row_part zeroes the term
+    const bf16_t *biases = w.biases ? w.biases : w.scales;
+    r.ok = w.biases ? 0x80000000u : 0u;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
         const int ch = li + c * lpr;
@@ -93,7 +96,7 @@ __device__ __forceinline__ void load_wrow(const QW &w, int e, int row, int li, i
         r.q[c] = *(const uint4 *)(codes + (size_t)chc * 4);
         const size_t gi = rr * groups + (chc * 32) / w.group;
         r.s[c] = w.scales[gi];
-        r.b[c] = w.biases ? (uint32_t)w.biases[gi] : 0u;
+        r.b[c] = biases[gi];
         r.ok |= (row < w.out && ch < n_ch) ? (1u << c) : 0u;
     }
 }
@@ -102,22 +105,26 @@ __device__ __forceinline__ void load_wrow(const QW &w, int e, int row, int li, i
 template <int CPL>
 __device__ __forceinline__ float row_part(const WRow<CPL> &r, const XChunk *x) {
     float a = 0.f;
+    const bool has_b = (r.ok >> 31) & 1u;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
         const bool ok = (r.ok >> c) & 1u;
         const float s = ok ? bf2f(r.s[c]) : 0.f;
-        const float bp = ok ? bf2f(r.b[c]) - 128.f * s : 0.f;
+        const float bp = ok ? (has_b ? bf2f(r.b[c]) : 0.f) - 128.f * s : 0.f;
         a += s * dot_chunk(r.q[c], x[c]) + bp * x[c].sum;
     }
     return a;
 }
 
-// Keeps packed codes opaque inside a loop so their conversion is not hoisted out of it.
+// Keeps a row's raw loads opaque inside a loop, so their conversions are not hoisted next to the
+// loads (where a conversion would wait for the load before the loads that follow are issued).
 template <int CPL>
 __device__ __forceinline__ void opaque_row(WRow<CPL> &r) {
 #pragma unroll
-    for (int c = 0; c < CPL; ++c)
+    for (int c = 0; c < CPL; ++c) {
         asm volatile("" : "+v"(r.q[c].x), "+v"(r.q[c].y), "+v"(r.q[c].z), "+v"(r.q[c].w));
+        asm volatile("" : "+v"(r.s[c]), "+v"(r.b[c]));
+    }
 }
 
 // The lane's chunks of one activation row (clamped: chunks past the row are masked by the

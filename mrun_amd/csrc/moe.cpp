@@ -264,7 +264,7 @@ namespace models {
 
 using Stages = StageMarks;
 
-static const char *kDecodeStages = "router_shared,gate_up,down_combine";
+static const char *kDecodeStages = "router,gate_up,down_combine";
 static const char *kPrefillStages =
     "router,shared_gate,topk,permute,gate_up,down,shared_gate_up,shared_down,combine";
 
