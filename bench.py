@@ -181,6 +181,38 @@ def cpu_baseline(hb, x_np, seconds: float):
                       f"block, OpenMP over {threads} threads; us/block {per * 1e6:.0f}"}
 
 
+def prefill_point(args, Q, M, synth, torch) -> dict:
+    """T = 2048 with the Zipf-skewed router."""
+    print("[bench] prefill configs[2] T=2048 (Zipf router)", file=sys.stderr, flush=True)
+    hz = synth.make_block(Q, config=synth.CFG_PREFILL_ZIPF, zipf=True)
+    dz = M.SparseMoe(hz)
+    T = 2048
+    xz = M.bf16_tensor(synth.make_x(Q, T, config=synth.CFG_PREFILL_ZIPF))
+    wall, dev_ms, _ = time_forward(dz, xz, max(args.steps // 10, 10), 3, torch)
+    stages = time_stages(dz, xz, 10, torch)
+    fl = prefill_flops(Q, T)
+    return {"tokens": T, "ms_per_step": wall, "device_ms": dev_ms,
+            "tokens_per_s": T / (wall * 1e-3), "us_per_layer": dev_ms * 1e3,
+            "stages_us": stages, "flops": fl,
+            "block_mfma_frac": fl["block"] / (dev_ms * 1e-3) / MFMA_BF16_PEAK,
+            "gate_up_mfma_frac": (fl["gate_up"] + fl["shared"] * 2 / 3)
+            / (stages["gate_up"] * 1e-6) / MFMA_BF16_PEAK,
+            "down_mfma_frac": (fl["down"] + fl["shared"] / 3)
+            / (stages["down"] * 1e-6) / MFMA_BF16_PEAK}
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 byte counters, or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    k = rec.get("kernels", {}).get(kernel)
+    return None if k is None else k.get("bytes_per_launch")
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -191,6 +223,8 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the configs[2] prefill point (for profilers); prints its own JSON line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device to device 10 times (the byte counters' reference)")
     args = ap.parse_args(argv)
@@ -214,6 +248,9 @@ def main(argv=None) -> int:
     from mrun_amd import synth
 
     Q = synth.QWEN36
+    if args.prefill_only:
+        print(json.dumps({"prefill": prefill_point(args, Q, M, synth, torch)}), flush=True)
+        return 0
     print(f"[bench] generating the configs[1] block ({Q.name})", file=sys.stderr, flush=True)
     hb = synth.make_block(Q, config=synth.CFG_DECODE)
     dev = M.SparseMoe(hb)
@@ -240,10 +277,12 @@ def main(argv=None) -> int:
     main_pt, x_main = decode_point(args.tokens, args.steps, args.warmup)
     gu_us = main_pt["stages_us"]["gate_up"]
     achieved = main_pt["bytes"]["gate_up"] / (gu_us * 1e-6)
-    roofline = {"kernel": "decode_gateup_kernel (routed + shared gate/up, SwiGLU fused)", "bound": "hbm",
+    kname = "decode_gateup_kernel"
+    roofline = {"kernel": f"{kname} (routed + shared gate/up, SwiGLU fused)", "bound": "hbm",
                 "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                "frac": achieved / HBM_PEAK, "traffic": None,
-                "bytes_per_launch": main_pt["bytes"]["gate_up"], "us_per_launch": gu_us}
+                "frac": achieved / HBM_PEAK, "traffic": measured_traffic(kname),
+                "bytes_per_launch": main_pt["bytes"]["gate_up"], "us_per_launch": gu_us,
+                "timing": "HIP events around the launch on its stream (includes the launch gap)"}
 
     sweep = []
     if not args.no_sweep:
@@ -254,23 +293,7 @@ def main(argv=None) -> int:
             p, _ = decode_point(T, max(args.steps // 2, 20), args.warmup)
             sweep.append(p)
 
-    prefill = None
-    if not args.no_prefill:
-        print("[bench] prefill configs[2] T=2048 (Zipf router)", file=sys.stderr, flush=True)
-        hz = synth.make_block(Q, config=synth.CFG_PREFILL_ZIPF, zipf=True)
-        dz = M.SparseMoe(hz)
-        T = 2048
-        xz = M.bf16_tensor(synth.make_x(Q, T, config=synth.CFG_PREFILL_ZIPF))
-        wall, dev_ms, _ = time_forward(dz, xz, max(args.steps // 10, 10), 3, torch)
-        stages = time_stages(dz, xz, 10, torch)
-        fl = prefill_flops(Q, T)
-        prefill = {"tokens": T, "ms_per_step": wall, "device_ms": dev_ms,
-                   "tokens_per_s": T / (wall * 1e-3), "us_per_layer": dev_ms * 1e3,
-                   "stages_us": stages, "flops": fl,
-                   "block_mfma_frac": fl["block"] / (dev_ms * 1e-3) / MFMA_BF16_PEAK,
-                   "gate_up_mfma_frac": fl["gate_up"] / (stages["gate_up"] * 1e-6) / MFMA_BF16_PEAK,
-                   "down_mfma_frac": fl["down"] / (stages["down"] * 1e-6) / MFMA_BF16_PEAK}
-        del dz, hz
+    prefill = None if args.no_prefill else prefill_point(args, Q, M, synth, torch)
 
     cpu = None
     if not args.no_cpu:
