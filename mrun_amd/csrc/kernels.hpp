@@ -163,7 +163,7 @@ struct GemmJob {
 hipError_t launch_gemm(const GemmJob &job, hipStream_t stream);
 // whether launch_gemm runs the 128-row kernel (4-bit, group 64 or 128), which also takes `sh`
 bool qgemm_supported(const GemmJob &job);
-constexpr int kGemmTileM = 128;  // rows per routed tile
+constexpr int kGemmTileM = 64;  // rows per routed tile
 constexpr int kGemmTileN = 64;
 
 // ---- elementwise ----

@@ -239,7 +239,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
 //    read the tile's A rows from it.
 //  - Optional shared tiles (a non-routed product of the same N, the shared expert) come first.
 
-constexpr int G_BM = 128, G_BNB = 256, G_KSC = 16, G_THREADS = 512;
+constexpr int G_BNB = 256, G_KSC = 16;
+// tile rows = 64 WM (WM waves along M), codes staged per SS K steps, SBUF buffers of scales
+constexpr int G_WM = 1, G_SS = 2, G_SBUF = 1, G_BM = 64 * G_WM, G_THREADS = 256 * G_WM;
 
 struct GTile {
     const bf16_t *A;
@@ -264,12 +266,13 @@ __device__ __forceinline__ uint32_t neg128_pair(uint32_t w) {
     return lo | hi;
 }
 
-template <bool GLU>
-__global__ __launch_bounds__(G_THREADS, 1) void qgemm_kernel(GemmJob j) {
-    __shared__ __align__(16) bf16_t As[2][G_BM * LDK];          // 36 KB
-    __shared__ __align__(16) uint4 Bc[2][G_BNB * 8];            // 64 KB: codes of a super-step
-    __shared__ __align__(16) bf16_t Sb[2][2][G_BNB][G_KSC];     // 32 KB: scales, biases of a chunk
-    __shared__ __align__(16) bf16_t Xs[2][3][G_BM][G_KSC];      // 24 KB: X splits of a chunk
+template <bool GLU, int WM, int SS, int SBUF>
+__global__ __launch_bounds__(256 * WM, 2 / WM) void qgemm_kernel(GemmJob j) {
+    constexpr int G_BM = 64 * WM, G_THREADS = 256 * WM, CU = 2 * SS;  // CU: 16-byte code units per row
+    __shared__ __align__(16) bf16_t As[2][G_BM * LDK];
+    __shared__ __align__(16) uint4 Bc[2][G_BNB * CU];           // codes of a super-step
+    __shared__ __align__(16) bf16_t Sb[SBUF][2][G_BNB][G_KSC];  // scales, biases of a chunk
+    __shared__ __align__(16) bf16_t Xs[2][3][G_BM][G_KSC];      // X splits of a chunk
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (j.zero && blockIdx.x == 0)
@@ -325,53 +328,72 @@ __global__ __launch_bounds__(G_THREADS, 1) void qgemm_kernel(GemmJob j) {
         const int col = min(n0 + (GLU ? (r % NCOLS) : r), j.N - 1);
         return (uint32_t)(g.e * wout + col);
     };
-    // codes: units u = tid + 512 i (i < 4) of a super-step: B row (tid / 8) + 64 i, 16-byte unit
-    // tid % 8; byte offsets (32-bit: the tensors stay below 4 GiB, checked by the host)
-    const uint32_t coff0 = weight_row((tid >> 3)) * (uint32_t)(K >> 1) + 16u * (tid & 7);
-    const uint32_t coff1 = weight_row((tid >> 3) + 64) * (uint32_t)(K >> 1) + 16u * (tid & 7);
-    const uint32_t coff2 = weight_row((tid >> 3) + 128) * (uint32_t)(K >> 1) + 16u * (tid & 7);
-    const uint32_t coff3 = weight_row((tid >> 3) + 192) * (uint32_t)(K >> 1) + 16u * (tid & 7);
-    const int cdst = (tid >> 3) * 8 + ((tid & 7) ^ ((tid >> 3) & 7));  // + 512 i
-    // scales (i = 0) / biases (i = 1): B row (tid / 2) % 256, 16-byte half tid % 2 of the chunk;
-    // offsets are clamped inside the tensor (a partial last chunk reads unused values)
-    const int sr = (tid >> 1) & 255;
-    const bool s_up = GLU && sr >= NCOLS;
-    const bf16_t *sbase = s_up ? scales1 : scales0, *bbase = s_up ? biases1 : biases0;
-    const uint32_t soff = weight_row(sr) * (uint32_t)groups + 8u * (tid & 1);  // in elements
+    // codes: units u = tid + G_THREADS i (i < 4) of a super-step, B row u / CU, 16-byte unit u % CU;
+    // the unit sits at position (u % CU) ^ swz(row) of its row, so fragment reads are free of
+    // bank conflicts; byte offsets are 32-bit (the tensors stay below 4 GiB, checked by the host)
+    auto swz = [](int r) { return CU == 8 ? ((r & 7) ^ ((r >> 3) & 1)) : (((r >> 1) & 3) ^ ((r >> 3) & 1)); };
+    constexpr int RPU = G_THREADS / CU;  // B rows covered by one unit index i
+    const int cr = tid / CU, cu = tid % CU;
+    const uint32_t coff0 = weight_row(cr) * (uint32_t)(K >> 1) + 16u * cu;
+    const uint32_t coff1 = weight_row(cr + RPU) * (uint32_t)(K >> 1) + 16u * cu;
+    const uint32_t coff2 = weight_row(cr + 2 * RPU) * (uint32_t)(K >> 1) + 16u * cu;
+    const uint32_t coff3 = weight_row(cr + 3 * RPU) * (uint32_t)(K >> 1) + 16u * cu;
+    const int cdst = cr * CU + (cu ^ swz(cr));  // + RPU * CU i (swz(cr + RPU i) == swz(cr))
+    // scales / biases of a chunk: units u = tid + G_THREADS i (i < 4 / WM): array u / 512, B row
+    // (u / 2) % 256, 16-byte half u % 2; offsets are clamped inside the tensor (a partial last
+    // chunk reads unused values)
+    constexpr int NSB = 4 / WM;
+    // unit i: array i / (NSB / 2) (scales, biases), B row (tid / 2) % 256 + 128 (i % (NSB / 2)) with
+    // WM = 1, (tid / 2) with WM = 2; two row offsets serve all units (named registers: arrays
+    // captured by the lambdas below would live in scratch)
+    const int sr0 = (tid >> 1) & 255, sr1 = NSB > 2 ? sr0 + 128 : sr0;
+    const uint32_t so0 = weight_row(sr0) * (uint32_t)groups + 8u * (tid & 1);  // in elements
+    const uint32_t so1 = weight_row(sr1) * (uint32_t)groups + 8u * (tid & 1);
+    const bool up0 = GLU && sr0 >= NCOLS, up1 = GLU && sr1 >= NCOLS;
+    const int sd0 = (sr0 * G_KSC + 8 * (tid & 1)) / 8, sd1 = (sr1 * G_KSC + 8 * (tid & 1)) / 8;
+    constexpr int SB_ARR = G_BNB * G_KSC / 8;  // uint4 per array
     const uint32_t slast = (uint32_t)wexp * (uint32_t)wout * (uint32_t)groups - 8u;
-    const int sdst = (sr * G_KSC + 8 * (tid & 1)) / 8;  // + 512 i, in uint4
     struct ARegs {
         uint4 a0, a1;
     };
-    uint4 rc0, rc1, rc2, rc3, rs0, rs1;  // codes of the next super-step, scales/biases of the next chunk
+    uint4 rc0, rc1, rc2, rc3;  // codes of the next super-step
+    uint4 rs0, rs1, rb0, rb1;  // scales and biases of the next chunk (rows sr0, sr1)
     auto load_a = [&](int ks, ARegs &r) __attribute__((always_inline)) {
         const uint4 *pa = (const uint4 *)(aptr + ks * BK);
         r.a0 = pa[0];
         r.a1 = pa[1];
     };
     auto load_codes = [&](int ss) __attribute__((always_inline)) {  // super-step ss (clamped by the caller)
-        const uint32_t o = 128u * (uint32_t)ss;
+        const uint32_t o = 32u * SS * (uint32_t)ss;
         rc0 = *(const uint4 *)((const char *)codes0 + coff0 + o);
         rc1 = *(const uint4 *)((const char *)codes0 + coff1 + o);
         rc2 = *(const uint4 *)((const char *)codes1 + coff2 + o);
         rc3 = *(const uint4 *)((const char *)codes1 + coff3 + o);
     };
     auto load_scales = [&](int ch) __attribute__((always_inline)) {  // chunk ch (clamped by the caller)
-        const uint32_t o = min(soff + (uint32_t)(ch * G_KSC), slast);
-        rs0 = *(const uint4 *)(sbase + o);
-        rs1 = *(const uint4 *)(bbase + o);
+        const uint32_t o = (uint32_t)(ch * G_KSC);
+        rs0 = *(const uint4 *)((up0 ? scales1 : scales0) + min(so0 + o, slast));
+        rb0 = *(const uint4 *)((up0 ? biases1 : biases0) + min(so0 + o, slast));
+        if (NSB > 2) {
+            rs1 = *(const uint4 *)((up1 ? scales1 : scales0) + min(so1 + o, slast));
+            rb1 = *(const uint4 *)((up1 ? biases1 : biases0) + min(so1 + o, slast));
+        }
     };
     auto store_codes = [&](int ss) __attribute__((always_inline)) {
         uint4 *d = &Bc[ss & 1][cdst];
         d[0] = rc0;
-        d[512] = rc1;
-        d[1024] = rc2;
-        d[1536] = rc3;
+        d[RPU * CU] = rc1;
+        d[2 * RPU * CU] = rc2;
+        d[3 * RPU * CU] = rc3;
     };
     auto store_scales = [&](int ch) __attribute__((always_inline)) {
-        uint4 *d = (uint4 *)&Sb[ch & 1][0][0][0] + sdst;
-        d[0] = rs0;
-        d[512] = rs1;
+        uint4 *d = (uint4 *)&Sb[ch % SBUF][0][0][0];
+        d[sd0] = rs0;
+        d[SB_ARR + sd0] = rb0;
+        if (NSB > 2) {
+            d[sd1] = rs1;
+            d[SB_ARR + sd1] = rb1;
+        }
     };
     auto stage_a = [&](const ARegs &r, int ks) __attribute__((always_inline)) {
         const int kc = ks % G_KSC, par = (ks / G_KSC) & 1, buf = ks & 1;
@@ -426,13 +448,14 @@ __global__ __launch_bounds__(G_THREADS, 1) void qgemm_kernel(GemmJob j) {
             for (int i = 0; i < 16; ++i) acc[mi][ni][i] = 0.f;
 
     auto compute = [&](int ks) __attribute__((always_inline)) {
-        const int kc = ks % G_KSC, buf = ks & 1, sb = (ks >> 2) & 1, par = (ks / G_KSC) & 1;
+        const int kc = ks % G_KSC, buf = ks & 1, sb = (ks / SS) & 1, par = (ks / G_KSC) & 1;
+        const int sbb = (ks / G_KSC) % SBUF;
         const bf16_t *as = As[buf];
         uint4 cw[2];
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni) {
-            const int R = bro[ni] + fr, c = 2 * (ks & 3) + fh;
-            cw[ni] = Bc[sb][R * 8 + (c ^ (R & 7))];
+            const int R = bro[ni] + fr, c = 2 * (ks % SS) + fh;
+            cw[ni] = Bc[sb][R * CU + (c ^ swz(R))];
         }
         f32x16_t part[2][2];
 #pragma unroll
@@ -460,7 +483,7 @@ __global__ __launch_bounds__(G_THREADS, 1) void qgemm_kernel(GemmJob j) {
         }
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni) {
-            const float sc = bf2f(Sb[par][0][bro[ni] + fr][kc]);
+            const float sc = bf2f(Sb[sbb][0][bro[ni] + fr][kc]);
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
@@ -471,8 +494,8 @@ __global__ __launch_bounds__(G_THREADS, 1) void qgemm_kernel(GemmJob j) {
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni) {
                 const int R = bro[ni] + fr;
-                const uint4 sv = *(const uint4 *)&Sb[par][0][R][fk];
-                bv[ni][0] = lds_frag(&Sb[par][1][R][fk]);
+                const uint4 sv = *(const uint4 *)&Sb[sbb][0][R][fk];
+                bv[ni][0] = lds_frag(&Sb[sbb][1][R][fk]);
                 bv[ni][1] = __builtin_bit_cast(
                     bf16x8_t, make_uint4(neg128_pair(sv.x), neg128_pair(sv.y), neg128_pair(sv.z),
                                          neg128_pair(sv.w)));
@@ -495,7 +518,7 @@ __global__ __launch_bounds__(G_THREADS, 1) void qgemm_kernel(GemmJob j) {
     };
 
     // ---- pipeline (nks is a multiple of 4)
-    const int nss = nks / 4, nch = (nks + G_KSC - 1) / G_KSC;
+    const int nss = nks / SS, nch = (nks + G_KSC - 1) / G_KSC;
     ARegs ra0, ra1;
     load_codes(0);
     load_scales(0);
@@ -513,9 +536,10 @@ __global__ __launch_bounds__(G_THREADS, 1) void qgemm_kernel(GemmJob j) {
         if (active) compute(k);
         if (k + 1 < nks) {
             if (super_end) {  // next super-step: its codes were loaded one super-step ago
-                store_codes((k + 1) >> 2);
-                load_codes(min(((k + 1) >> 2) + 1, nss - 1));
+                store_codes((k + 1) / SS);
+                load_codes(min((k + 1) / SS + 1, nss - 1));
                 if ((k + 1) % G_KSC == 0) {
+                    if (SBUF == 1) __syncthreads();  // every wave is done with the chunk's scales
                     store_scales((k + 1) / G_KSC);
                     load_scales(min((k + 1) / G_KSC + 1, nch - 1));
                 }
@@ -526,9 +550,9 @@ __global__ __launch_bounds__(G_THREADS, 1) void qgemm_kernel(GemmJob j) {
         __syncthreads();
     };
     for (int ks = 0; ks < nks; ks += 4) {
-        step(ks, false, ra1);
-        step(ks + 1, false, ra0);
-        step(ks + 2, false, ra1);
+        step(ks, SS == 1, ra1);
+        step(ks + 1, SS <= 2, ra0);
+        step(ks + 2, SS == 1, ra1);
         step(ks + 3, true, ra0);
     }
     if (!active) return;
@@ -589,8 +613,8 @@ hipError_t launch_gemm(const GemmJob &j, hipStream_t stream) {
         const int tiles8 = (s_tiles + r_tiles + 7) / 8 * 8;
         if (tiles8 == 0) return hipSuccess;
         const dim3 grid(tiles8 * nblk);
-        if (j.glu) qgemm_kernel<true><<<grid, G_THREADS, 0, stream>>>(j);
-        else qgemm_kernel<false><<<grid, G_THREADS, 0, stream>>>(j);
+        if (j.glu) qgemm_kernel<true, G_WM, G_SS, G_SBUF><<<grid, G_THREADS, 0, stream>>>(j);
+        else qgemm_kernel<false, G_WM, G_SS, G_SBUF><<<grid, G_THREADS, 0, stream>>>(j);
         return hipGetLastError();
     }
     if (j.has_shared) return hipErrorInvalidValue;  // only the kernel above takes shared tiles
