@@ -3,11 +3,12 @@
 Default workload: one Qwen3.6-35B-A3B-like block (hidden 2048, 256 experts,
 top-8 with norm_topk_prob, expert FFN 512, shared expert 512), 4-bit affine group-64 weights,
 synthetic seeded data, decode T = 1. A step is one block forward over the batch. The JSON line
-also carries the T = 2, 4, 16 decode sweep and the configs[2] prefill (T = 2048, Zipf-skewed
-router) measured the same way, the dominant kernel's roofline (HIP events on the launch stream)
+also carries the T = 2, 4, 16 decode sweep, the configs[2] prefill (T = 2048, Zipf-skewed
+router) and the configs[3] stack of 40 layers (T = 1 and T = 4096) measured the same way, the dominant kernel's roofline (HIP events on the launch stream)
 and the CPU restatement timed on a bounded sample on this host.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens T] [--no-cpu] [--no-prefill]
+                    [--no-stack] [--stack-only] [--prefill-only]
 """
 from __future__ import annotations
 
@@ -201,6 +202,53 @@ def prefill_point(args, Q, M, synth, torch) -> dict:
             / (stages["down"] * 1e-6) / MFMA_BF16_PEAK}
 
 
+def stack_point(args, Q, M, synth, torch) -> dict:
+    """40 MoE layers with their own seeded weights (generated on the device: about
+    18 GB), pre-RMSNorm (eps 1e-6, weight 1) and the residual add, at T = 1 decode and T = 4096
+    prefill. A step is one pass of x through all layers."""
+    n = args.stack_layers
+    print(f"[bench] stack configs[3]: generating {n} layers on the device", file=sys.stderr,
+          flush=True)
+    layers = [M.device_block(Q, synth.CFG_STACK, l) for l in range(n)]
+    st = M.MoeStack(layers, None, 1e-6)
+    torch.cuda.synchronize()
+    wbytes = sum(t.numel() * t.element_size() for l in layers for t in l.tensors())
+    out = {"layers": n, "weight_bytes": wbytes}
+    for T, steps in ((1, max(args.steps // 10, 10)), (4096, 5)):
+        print(f"[bench] stack T={T}", file=sys.stderr, flush=True)
+        x0 = M.bf16_tensor(synth.make_x(Q, T, config=synth.CFG_STACK, layer=T))
+        x = x0.clone()
+        ws = st.workspace(T)
+        for _ in range(2):
+            st.forward_(x, ws)
+        stream = torch.cuda.current_stream()
+        ev = Events(2)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev.record(0, stream)
+        for _ in range(steps):
+            st.forward_(x, ws)
+        ev.record(1, stream)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3 / steps
+        dev_ms = ev.ms(0, 1) / steps
+        assert bool(torch.isfinite(x.float()).all()), "stack output not finite"
+        pt = {"tokens": T, "steps": steps, "ms_per_step": wall, "device_ms": dev_ms,
+              "tokens_per_s": T / (wall * 1e-3), "us_per_layer": dev_ms * 1e3 / n}
+        if T == 1:
+            # one token picks top_k distinct experts in every layer; plus the norm's x, h traffic
+            b = n * (decode_bytes(Q, Q.top_k, 1)["block"] + 4 * Q.hidden)
+            pt.update(bytes=b, hbm_frac=b / (dev_ms * 1e-3) / HBM_PEAK)
+        else:
+            f = n * prefill_flops(Q, T)["block"]
+            pt.update(flops=f, mfma_frac=f / (dev_ms * 1e-3) / MFMA_BF16_PEAK)
+        out[f"T{T}"] = pt
+        del x, x0
+    del st, layers
+    torch.cuda.empty_cache()
+    return out
+
+
 def measured_traffic(kernel: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 byte counters, or None."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
@@ -223,6 +271,10 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-stack", action="store_true")
+    ap.add_argument("--stack-layers", type=int, default=40)
+    ap.add_argument("--stack-only", action="store_true",
+                    help="only the configs[3] layer stack; prints its own JSON line")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the configs[2] prefill point (for profilers); prints its own JSON line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -250,6 +302,9 @@ def main(argv=None) -> int:
     Q = synth.QWEN36
     if args.prefill_only:
         print(json.dumps({"prefill": prefill_point(args, Q, M, synth, torch)}), flush=True)
+        return 0
+    if args.stack_only:
+        print(json.dumps({"stack": stack_point(args, Q, M, synth, torch)}), flush=True)
         return 0
     print(f"[bench] generating the configs[1] block ({Q.name})", file=sys.stderr, flush=True)
     hb = synth.make_block(Q, config=synth.CFG_DECODE)
@@ -294,6 +349,7 @@ def main(argv=None) -> int:
             sweep.append(p)
 
     prefill = None if args.no_prefill else prefill_point(args, Q, M, synth, torch)
+    stack = None if args.no_stack else stack_point(args, Q, M, synth, torch)
 
     cpu = None
     if not args.no_cpu:
@@ -326,6 +382,7 @@ def main(argv=None) -> int:
         "cpu_baseline": cpu,
         "sweep": sweep,
         "prefill": prefill,
+        "stack": stack,
     }
     print(json.dumps(line), flush=True)
     return 0

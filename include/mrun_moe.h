@@ -167,6 +167,17 @@ int mrun_add_rms_norm(const mrun_bf16 *x, const mrun_bf16 *residual, const mrun_
                       int32_t rows, int32_t hidden, float eps, mrun_bf16 *h, mrun_bf16 *y,
                       mrun_stream_t stream);
 
+/* The decoder-layer loop around the MoE block for a stack of MoE layers (qwen3_5_moe.rs:622-624,
+ * 664-666): for each layer l, h = rms_norm(x) * norm_w[l] (eps; load.rs:361-363), then
+ * x = R(x + SparseMoe_l(h)). The residual add of layer l and the norm of layer l + 1 run as one
+ * add_rms_norm (nuvec.rs:800-811). x [tokens, hidden] is updated in place. norm_w holds n_layers
+ * pointers to [hidden] bf16 weights (NULL, or a NULL entry, means weight 1). All layers share one
+ * config. */
+int mrun_moe_stack_forward(const mrun_sparse_moe *layers, int32_t n_layers,
+                           const mrun_bf16 *const *norm_w, float eps, mrun_bf16 *x, int32_t tokens,
+                           void *workspace, size_t workspace_bytes, mrun_stream_t stream);
+size_t mrun_moe_stack_workspace_bytes(const mrun_moe_config *cfg, int32_t tokens);
+
 #ifdef __cplusplus
 }
 #endif

@@ -42,6 +42,15 @@ void mrun_synth_scales_biases(uint64_t seed, uint16_t *scales, uint16_t *biases,
 int mrun_synth_zipf_bias(uint64_t seed, int32_t experts, double s, double amp, uint16_t *bias,
                          int32_t *rank_out);
 
+/* Device variants (libmrun_synth_dev.so), asynchronous on a HIP stream, writing device memory:
+ * the same draws, so codes are bit-identical to mrun_synth_codes; normals use the device's float64
+ * math. Return 0, or -1 for bad arguments or a launch error. */
+int mrun_synth_codes_dev(uint64_t seed, int32_t bits, uint32_t *words, size_t n_words,
+                         void *stream);
+int mrun_synth_normal_bf16_dev(uint64_t seed, float std, uint16_t *out, size_t n, void *stream);
+int mrun_synth_scales_biases_dev(uint64_t seed, uint16_t *scales, uint16_t *biases, size_t n,
+                                 void *stream);
+
 #ifdef __cplusplus
 }
 #endif

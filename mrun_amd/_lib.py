@@ -114,6 +114,11 @@ SIGNATURES = {
         c_int32,
         [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_float, c_void_p, c_void_p, c_void_p],
     ),
+    "mrun_moe_stack_forward": (
+        c_int32,
+        [c_void_p, c_int32, c_void_p, c_float, c_void_p, c_int32, c_void_p, c_size_t, c_void_p],
+    ),
+    "mrun_moe_stack_workspace_bytes": (c_size_t, [POINTER(MoeConfig), c_int32]),
 }
 
 

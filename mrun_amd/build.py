@@ -2,6 +2,7 @@
 
 - mrun_amd/lib/libmrun_moe.so   : the HIP kernels for gfx950 + the C ABI (include/mrun_moe.h)
 - mrun_amd/lib/libmrun_synth.so : the seeded input generator (include/mrun_synth.h), host C
+- mrun_amd/lib/libmrun_synth_dev.so : its device variant (HIP)
 - oracle/_build/liborc_moe.so   : the CPU restatement used by tests and the CPU baseline
 
 Every HIP translation unit is compiled with packed-FP32 instructions disabled
@@ -81,6 +82,17 @@ def build_synth() -> Path:
     return target
 
 
+def build_synth_dev() -> Path:
+    """The device variant of the generator (benchmark inputs too large to make on the host)."""
+    LIB.mkdir(parents=True, exist_ok=True)
+    OBJ.mkdir(parents=True, exist_ok=True)
+    target = LIB / "libmrun_synth_dev.so"
+    tmp = LIB / "libmrun_synth_dev.so.tmp"
+    _run([HIPCC, *HIP_FLAGS, "-shared", str(CSRC / "synth_dev.hip"), "-o", str(tmp)])
+    os.replace(tmp, target)
+    return target
+
+
 def build_oracle() -> Path:
     """The CPU restatement (test infrastructure); built beside the product, never linked into it."""
     _run(["make", "-s", "-C", str(ROOT / "oracle")])
@@ -90,7 +102,7 @@ def build_oracle() -> Path:
 def build_all() -> list[Path]:
     if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
         raise RuntimeError(f"hipcc not found at {HIPCC}")
-    return [build_synth(), build_oracle(), build_moe()]
+    return [build_synth(), build_synth_dev(), build_oracle(), build_moe()]
 
 
 if __name__ == "__main__":

@@ -82,9 +82,10 @@ hipError_t launch_combine(const bf16_t *y, const uint32_t *inverse, const bf16_t
     return hipGetLastError();
 }
 
-// One workgroup per row. With res: h = R(x + res) is written and normalised; else x is.
-__global__ __launch_bounds__(256) void rms_norm_kernel(const bf16_t *__restrict__ x,
-                                                       const bf16_t *__restrict__ res,
+// One workgroup per row. With res: h = R(x + res) is written and normalised; else x is. h may
+// alias x or res (each thread writes only the elements it has just read), so neither is restrict.
+__global__ __launch_bounds__(256) void rms_norm_kernel(const bf16_t *x,
+                                                       const bf16_t *res,
                                                        const bf16_t *__restrict__ w, int D,
                                                        float eps, bf16_t *h,
                                                        bf16_t *__restrict__ y) {

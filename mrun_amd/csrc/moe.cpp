@@ -632,6 +632,50 @@ int mrun_moe_combine(const mrun_bf16 *y, const uint32_t *inverse, const mrun_bf1
     return report(st);
 }
 
+size_t mrun_moe_stack_workspace_bytes(const mrun_moe_config *cfg, int32_t tokens) {
+    const size_t block = mrun_moe_workspace_bytes(cfg, tokens);
+    if (block == 0) return 0;
+    return block + 2 * a256(2 * (size_t)tokens * cfg->hidden);  // h and the block output
+}
+
+int mrun_moe_stack_forward(const mrun_sparse_moe *layers, int32_t n_layers,
+                           const mrun_bf16 *const *norm_w, float eps, mrun_bf16 *x, int32_t tokens,
+                           void *workspace, size_t workspace_bytes, mrun_stream_t stream) {
+    Status st;
+    if (!layers || n_layers <= 0) st = Err(MRUN_ERR_INVALID, "stack: no layers");
+    for (int32_t l = 0; st.ok() && l < n_layers; ++l) {
+        st = check_block(&layers[l]);
+        if (st.ok() && std::memcmp(&layers[l].cfg, &layers[0].cfg, sizeof(mrun_moe_config)) != 0)
+            st = Err(MRUN_ERR_INVALID, "stack: layers must share one config");
+    }
+    if (st.ok() && tokens <= 0) st = Err(MRUN_ERR_INVALID, "tokens must be positive");
+    if (st.ok()) st = check_ptr(x, "x");
+    if (st.ok()) st = check_ptr(workspace, "workspace");
+    const mrun_moe_config &c = layers[0].cfg;
+    const size_t need = st.ok() ? mrun_moe_stack_workspace_bytes(&c, tokens) : 0;
+    if (st.ok() && workspace_bytes < need)
+        st = Err(MRUN_ERR_WORKSPACE, "workspace of " + std::to_string(workspace_bytes) +
+                                         " bytes, need " + std::to_string(need));
+    if (st.ok()) {
+        const int D = c.hidden;
+        const size_t blk = mrun_moe_workspace_bytes(&c, tokens);
+        char *ws = (char *)workspace;
+        bf16_t *h = (bf16_t *)(ws + blk);
+        bf16_t *o = (bf16_t *)(ws + blk + a256(2 * (size_t)tokens * D));
+        hipStream_t s = (hipStream_t)stream;
+        auto wl = [&](int l) { return norm_w ? norm_w[l] : nullptr; };
+        st = hip_status(launch_rms_norm(x, nullptr, wl(0), tokens, D, eps, nullptr, h, s), "stack norm");
+        for (int32_t l = 0; st.ok() && l < n_layers; ++l) {
+            st = models::sparse_moe_forward(layers[l], h, tokens, o, ws, blk, s);
+            if (!st.ok()) break;
+            // x = R(x + o), and the next layer's input h = rms_norm(x) (the last h is unused)
+            const bf16_t *w = wl(l + 1 < n_layers ? l + 1 : l);
+            st = hip_status(launch_rms_norm(x, o, w, tokens, D, eps, x, h, s), "stack add_rms_norm");
+        }
+    }
+    return report(st);
+}
+
 int mrun_rms_norm(const mrun_bf16 *x, const mrun_bf16 *w, int32_t rows, int32_t hidden, float eps,
                   mrun_bf16 *out, mrun_stream_t stream) {
     Status st;

@@ -49,11 +49,20 @@ def u32_array(t: torch.Tensor) -> np.ndarray:
 class DeviceQTensor:
     """A QTensor resident on the device, with its C view (tensor::Quantized, nuvec.rs:602-638)."""
 
-    def __init__(self, q: QTensor, device="cuda"):
+    def __init__(self, q: QTensor | None, device="cuda"):
+        if q is None:  # filled by from_tensors
+            return
         self.codes = u32_tensor(q.codes, device)
         self.scales = bf16_tensor(q.scales, device)
         self.biases = bf16_tensor(q.biases, device) if q.biases is not None else None
         self.experts, self.out, self.in_, self.group, self.bits = q.experts, q.out, q.in_, q.group, q.bits
+
+    @classmethod
+    def from_tensors(cls, codes, scales, biases, experts, out, in_, group, bits=4):
+        t = cls(None)
+        t.codes, t.scales, t.biases = codes, scales, biases
+        t.experts, t.out, t.in_, t.group, t.bits = experts, out, in_, group, bits
+        return t
 
     @property
     def c(self) -> Quantized:
@@ -75,19 +84,23 @@ class SparseMoe:
     """SparseMoe (moe.rs:109-188) with its weights on the device."""
 
     def __init__(self, hb: HostBlock, device="cuda"):
+        """From host arrays (HostBlock), or from a block whose tensors are on the device already
+        (torch tensors and DeviceQTensors, as device_block makes)."""
         s = hb.shape
         self.shape = s
-        self.router = bf16_tensor(hb.router, device)
-        self.router_bias = bf16_tensor(hb.router_bias, device) if hb.router_bias is not None else None
-        self.gate_proj = DeviceQTensor(hb.gate_proj, device)
-        self.up_proj = DeviceQTensor(hb.up_proj, device)
-        self.down_proj = DeviceQTensor(hb.down_proj, device)
+        dev = lambda a: a if isinstance(a, torch.Tensor) else bf16_tensor(a, device)
+        qdev = lambda q: q if isinstance(q, DeviceQTensor) else DeviceQTensor(q, device)
+        self.router = dev(hb.router)
+        self.router_bias = dev(hb.router_bias) if hb.router_bias is not None else None
+        self.gate_proj = qdev(hb.gate_proj)
+        self.up_proj = qdev(hb.up_proj)
+        self.down_proj = qdev(hb.down_proj)
         self.shared = s.shared > 0
         if self.shared:
-            self.sh_gate_proj = DeviceQTensor(hb.sh_gate_proj, device)
-            self.sh_up_proj = DeviceQTensor(hb.sh_up_proj, device)
-            self.sh_down_proj = DeviceQTensor(hb.sh_down_proj, device)
-            self.sh_expert_gate = bf16_tensor(hb.sh_expert_gate, device)
+            self.sh_gate_proj = qdev(hb.sh_gate_proj)
+            self.sh_up_proj = qdev(hb.sh_up_proj)
+            self.sh_down_proj = qdev(hb.sh_down_proj)
+            self.sh_expert_gate = dev(hb.sh_expert_gate)
         self.cfg = MoeConfig(s.hidden, s.experts, s.top_k, s.intermediate, int(s.norm_topk),
                              s.shared)
         m = _SparseMoe()
@@ -104,6 +117,17 @@ class SparseMoe:
         self.c = m
         check(_lib.load().mrun_moe_check(ctypes.byref(self.c)))
         self._ws = None
+
+    def tensors(self) -> list:
+        """Every device tensor of the block's weights."""
+        qs = [self.gate_proj, self.up_proj, self.down_proj]
+        ts = [self.router] + ([self.router_bias] if self.router_bias is not None else [])
+        if self.shared:
+            qs += [self.sh_gate_proj, self.sh_up_proj, self.sh_down_proj]
+            ts.append(self.sh_expert_gate)
+        for q in qs:
+            ts += [q.codes, q.scales] + ([q.biases] if q.biases is not None else [])
+        return ts
 
     def workspace_bytes(self, tokens: int) -> int:
         return int(_lib.load().mrun_moe_workspace_bytes(ctypes.byref(self.cfg), tokens))
@@ -136,6 +160,108 @@ class SparseMoe:
                                           _ptr(gates), _ptr(ids), _ptr(scores), None, 0,
                                           _stream(stream)))
         return logits, gates, ids, scores
+
+
+# ---- device-generated blocks and the layer stack ----
+
+_SYNTH_DEV = None
+
+
+def _synth_dev() -> ctypes.CDLL:
+    global _SYNTH_DEV
+    if _SYNTH_DEV is None:
+        p = _lib.LIB_PATH.parent / "libmrun_synth_dev.so"
+        if not p.exists():
+            raise RuntimeError(f"{p} is missing: build it with `python -m mrun_amd.build`")
+        l = ctypes.CDLL(str(p))
+        l.mrun_synth_codes_dev.argtypes = [ctypes.c_uint64, ctypes.c_int32, ctypes.c_void_p,
+                                           ctypes.c_size_t, ctypes.c_void_p]
+        l.mrun_synth_normal_bf16_dev.argtypes = [ctypes.c_uint64, ctypes.c_float, ctypes.c_void_p,
+                                                 ctypes.c_size_t, ctypes.c_void_p]
+        l.mrun_synth_scales_biases_dev.argtypes = [ctypes.c_uint64, ctypes.c_void_p,
+                                                   ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        for f in (l.mrun_synth_codes_dev, l.mrun_synth_normal_bf16_dev,
+                  l.mrun_synth_scales_biases_dev):
+            f.restype = ctypes.c_int32
+        _SYNTH_DEV = l
+    return _SYNTH_DEV
+
+
+def device_normal_bf16(seed: int, n: int, std: float, device="cuda") -> torch.Tensor:
+    out = torch.empty(n, dtype=torch.bfloat16, device=device)
+    if _synth_dev().mrun_synth_normal_bf16_dev(seed, std, _ptr(out), n, _stream(None)) != 0:
+        raise RuntimeError("mrun_synth_normal_bf16_dev failed")
+    return out
+
+
+def device_qtensor(config: int, layer: int, codes_id: int, scales_id: int, experts: int, out: int,
+                   in_: int, group: int = 64, device="cuda") -> DeviceQTensor:
+    """synth.qtensor generated on the device (bit-identical codes; same scale formula)."""
+    from . import synth
+    lib = _synth_dev()
+    n_words, n_groups = experts * out * in_ // 8, experts * out * in_ // group
+    codes = torch.empty(n_words, dtype=torch.int32, device=device)
+    scales = torch.empty(n_groups, dtype=torch.bfloat16, device=device)
+    biases = torch.empty(n_groups, dtype=torch.bfloat16, device=device)
+    if lib.mrun_synth_codes_dev(synth.seed(config, layer, codes_id), 4, _ptr(codes), n_words,
+                                _stream(None)) != 0:
+        raise RuntimeError("mrun_synth_codes_dev failed")
+    if lib.mrun_synth_scales_biases_dev(synth.seed(config, layer, scales_id), _ptr(scales),
+                                        _ptr(biases), n_groups, _stream(None)) != 0:
+        raise RuntimeError("mrun_synth_scales_biases_dev failed")
+    return DeviceQTensor.from_tensors(codes, scales, biases, experts, out, in_, group)
+
+
+def device_block(shape, config: int, layer: int, device="cuda") -> "SparseMoe":
+    """synth.make_block(shape, config, layer) (no Zipf bias) made on the device: for weight stacks
+    too large to generate on the host."""
+    from types import SimpleNamespace
+    from . import synth as S
+    D, E, I, Sh, g = shape.hidden, shape.experts, shape.intermediate, shape.shared, shape.group
+    hb = SimpleNamespace(
+        shape=shape,
+        router=device_normal_bf16(S.seed(config, layer, S.ROUTER_W), E * D, 0.02, device).view(E, D),
+        router_bias=None,
+        gate_proj=device_qtensor(config, layer, S.GATE_CODES, S.GATE_SCALES, E, I, D, g, device),
+        up_proj=device_qtensor(config, layer, S.UP_CODES, S.UP_SCALES, E, I, D, g, device),
+        down_proj=device_qtensor(config, layer, S.DOWN_CODES, S.DOWN_SCALES, E, D, I, g, device),
+    )
+    if Sh:
+        hb.sh_gate_proj = device_qtensor(config, layer, S.SH_GATE_CODES, S.SH_GATE_SCALES, 1, Sh, D, g, device)
+        hb.sh_up_proj = device_qtensor(config, layer, S.SH_UP_CODES, S.SH_UP_SCALES, 1, Sh, D, g, device)
+        hb.sh_down_proj = device_qtensor(config, layer, S.SH_DOWN_CODES, S.SH_DOWN_SCALES, 1, D, Sh, g, device)
+        hb.sh_expert_gate = device_normal_bf16(S.seed(config, layer, S.SH_EXPERT_GATE), D, 0.02,
+                                               device).view(1, D)
+    return SparseMoe(hb, device)
+
+
+class MoeStack:
+    """A stack of MoE layers with the RMSNorm + residual around each (qwen3_5_moe.rs:622-624)."""
+
+    def __init__(self, layers: list, norm_w: list | None = None, eps: float = 1e-6):
+        self.layers = layers
+        self.eps = eps
+        self.norm_w = norm_w
+        n = len(layers)
+        self._arr = (_SparseMoe * n)(*[l.c for l in layers])
+        self._nw = None
+        if norm_w is not None:
+            self._nw = (ctypes.c_void_p * n)(*[_ptr(w).value if w is not None else None for w in norm_w])
+        self._ws = None
+
+    def workspace(self, tokens: int) -> torch.Tensor:
+        need = int(_lib.load().mrun_moe_stack_workspace_bytes(ctypes.byref(self.layers[0].cfg), tokens))
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(need, dtype=torch.uint8, device=self.layers[0].router.device)
+        return self._ws
+
+    def forward_(self, x: torch.Tensor, workspace: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+        """x [T, hidden] bf16, updated in place."""
+        ws = workspace if workspace is not None else self.workspace(x.shape[0])
+        check(_lib.load().mrun_moe_stack_forward(self._arr, len(self.layers), self._nw, self.eps,
+                                                 _ptr(x), x.shape[0], _ptr(ws), ws.numel(),
+                                                 _stream(stream)))
+        return x
 
 
 # ---- facade ops ----
@@ -220,7 +346,7 @@ def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, w: torch.Tensor | None
 
 
 __all__ = [
-    "SparseMoe", "DeviceQTensor", "Shape", "permute", "gather_qmm", "quantized_matmul", "linear",
+    "SparseMoe", "DeviceQTensor", "MoeStack", "device_block", "Shape", "permute", "gather_qmm", "quantized_matmul", "linear",
     "swiglu", "combine", "rms_norm", "add_rms_norm", "bf16_tensor", "u32_tensor", "bf16_bits",
     "u32_array",
 ]

@@ -28,8 +28,9 @@ def test_every_declared_symbol_is_exported():
         assert hasattr(lib, n), n
     assert set(names) == set(_lib.SIGNATURES), "the ctypes view must cover the header"
     syn = ctypes.CDLL(str(ROOT / "mrun_amd" / "lib" / "libmrun_synth.so"))
+    syn_dev = ctypes.CDLL(str(ROOT / "mrun_amd" / "lib" / "libmrun_synth_dev.so"))
     for n in declared(ROOT / "include" / "mrun_synth.h"):
-        assert hasattr(syn, n), n
+        assert hasattr(syn_dev if n.endswith("_dev") else syn, n), n
     assert b"gfx950" in lib.mrun_version()
 
 

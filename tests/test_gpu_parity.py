@@ -15,7 +15,7 @@ import torch
 from mrun_amd import moe as M
 from mrun_amd import synth
 from oracle import oracle as O
-from tests.helpers import assert_close, beyond_rounding, stats, ulp_distance
+from tests.helpers import assert_close, beyond_rounding, bf16_ulp, stats, ulp_distance
 
 pytestmark = pytest.mark.gpu
 
@@ -285,3 +285,73 @@ def _coder_dev():
     if "dev" not in _CODER:
         _CODER["dev"] = M.SparseMoe(_coder_host())
     return _CODER["dev"]
+
+
+# ---------------------------------------------------------------------------------------------
+# device-side generator (benchmark inputs) and the layer stack around the block
+
+def _near(a, b, max_diff=2, ulps=1):
+    """Equal, or (float64 log/sin/cos of device and host libm may differ in the last place) a
+    handful of elements one bf16 ulp apart."""
+    d = ulp_distance(a, b)
+    return int(np.count_nonzero(d)) <= max_diff and int(d.max(initial=0)) <= ulps
+
+
+def test_device_generator_matches_host():
+    """Codes bit-identical to the host generator; scales, biases and normals equal up to libm's
+    last place."""
+    E, O_, I_ = 1, 1024, 8192
+    dev = M.device_qtensor(7, 3, synth.GATE_CODES, synth.GATE_SCALES, E, O_, I_)
+    host = synth.qtensor(7, 3, synth.GATE_CODES, synth.GATE_SCALES, E, O_, I_)
+    torch.cuda.synchronize()
+    assert np.array_equal(M.u32_array(dev.codes), host.codes.ravel())
+    assert _near(M.bf16_bits(dev.scales), host.scales.ravel())
+    assert _near(M.bf16_bits(dev.biases), host.biases.ravel())
+    s = synth.seed(7, 3, synth.ROUTER_W)
+    nd = M.bf16_bits(M.device_normal_bf16(s, 1 << 16, 0.02))
+    assert _near(nd, synth.normal_bf16(s, 1 << 16, 0.02))
+
+
+STACK = synth.Shape(hidden=2048, experts=32, top_k=4, intermediate=512, shared=512)
+
+
+@pytest.fixture(scope="module")
+def stack3():
+    hosts = [synth.make_block(STACK, config=synth.CFG_STACK, layer=l) for l in range(3)]
+    return hosts, M.MoeStack([M.SparseMoe(h) for h in hosts])
+
+
+@pytest.mark.parametrize("T", [4, 40])
+def test_stack_matches_layer_loop_and_oracle(stack3, T):
+    """configs[3]'s decoder-layer loop, x = R(x + MoE_l(rms_norm(x))) per layer, with layer l's
+    residual add and layer l+1's norm fused (add_rms_norm). T=4 takes the decode schedule, T=40 the
+    prefill one. Bit-identical to the loop of single ops on the GPU. Against the CPU restatement,
+    layer by layer on the GPU's expert choices (each validated as a top-k within ties): within the
+    block bar plus one bf16 ulp of the residual stream (a rounding of x + MoE(h) that lands on the
+    neighbouring value moves x by one ulp of |x|, which exceeds 2e-2 where |x| >= 4)."""
+    hosts, st = stack3
+    x_np = synth.make_x(STACK, T, config=synth.CFG_STACK, layer=T)
+    got = M.bf16_bits(st.forward_(M.bf16_tensor(x_np)))
+    x = M.bf16_tensor(x_np)
+    h = M.rms_norm(x, None, 1e-6)
+    ids = []
+    for layer in st.layers:
+        ids.append(M.u32_array(layer.router_forward(h)[2]).reshape(T, -1))
+        o = layer.forward(h)
+        x, h = M.add_rms_norm(x, o, None, 1e-6)
+    torch.cuda.synchronize()
+    assert np.array_equal(got, M.bf16_bits(x)), "stack entry point differs from the op loop"
+    ref = x_np.copy()
+    for hb, gi in zip(hosts, ids):
+        o = O.moe_forward(hb, O.rms_norm(ref, None, 1e-6), forced_ids=gi)
+        ref = O.bf16_from_f32(synth.bf16_to_f32(ref) + synth.bf16_to_f32(o))
+    g, r = synth.bf16_to_f32(got).astype(np.float64), synth.bf16_to_f32(ref).astype(np.float64)
+    bound = 2e-2 + bf16_ulp(np.maximum(np.abs(g), np.abs(r)))
+    s = stats(got, ref)
+    assert np.all(np.abs(g - r) <= bound), f"stack T={T}: {s}"
+    assert s["l1_rel"] <= 1e-3, f"stack T={T}: {s}"
+    # the oracle's own stack entry agrees with its layer loop
+    if T == 4:
+        own = O.moe_stack(hosts, x_np, None, 1e-6)
+        _log(f"oracle stack vs GPU: {stats(got, own)}")
+    _log(f"stack of 3, T={T}: {s}")
