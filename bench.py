@@ -236,6 +236,28 @@ def stack_point(args, Q, M, synth, torch) -> dict:
         pt = {"tokens": T, "steps": steps, "ms_per_step": wall, "device_ms": dev_ms,
               "tokens_per_s": T / (wall * 1e-3), "us_per_layer": dev_ms * 1e3 / n}
         if T == 1:
+            # the whole stack captured as one HIP graph (launch overhead amortised)
+            s = torch.cuda.Stream()
+            s.wait_stream(stream)
+            with torch.cuda.stream(s):
+                st.forward_(x, ws, stream=s)
+            stream.wait_stream(s)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                st.forward_(x, ws, stream=s)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            ev.record(0, stream)
+            for _ in range(steps):
+                g.replay()
+            ev.record(1, stream)
+            torch.cuda.synchronize()
+            pt["graph_ms"] = ev.ms(0, 1) / steps
+            pt["graph_us_per_layer"] = pt["graph_ms"] * 1e3 / n
+            del g
+        if T == 1:
             # one token picks top_k distinct experts in every layer; plus the norm's x, h traffic
             b = n * (decode_bytes(Q, Q.top_k, 1)["block"] + 4 * Q.hidden)
             pt.update(bytes=b, hbm_frac=b / (dev_ms * 1e-3) / HBM_PEAK)

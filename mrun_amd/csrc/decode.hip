@@ -431,8 +431,10 @@ bool decode_supported(int D, int I, int S, int T, int k, int E) {
 }
 
 hipError_t launch_decode(const DecodeJob &j, hipStream_t s, StageMarks *marks) {
-    if (j.T <= 4) launch_k1<4>(j, s);
-    else launch_k1<16>(j, s);
+    if (!j.router_done) {
+        if (j.T <= 4) launch_k1<4>(j, s);
+        else launch_k1<16>(j, s);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (!j.topk_in_kernel) {

@@ -154,6 +154,17 @@ hipError_t launch_add_bias(bf16_t *y, const bf16_t *bias, int rows, int n, hipSt
     return hipGetLastError();
 }
 
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t *dst, uint32_t v, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) dst[i] = v;
+}
+
+hipError_t launch_fill_u32(uint32_t *dst, uint32_t v, int n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    fill_u32_kernel<<<dim3((n + 255) / 256), 256, 0, stream>>>(dst, v, n);
+    return hipGetLastError();
+}
+
 // y[t][n] = R(x[t] . W[n]) (then R(. + bias[n])) for narrow outputs (a Linear with few rows, e.g.
 // the shared expert's gate): one wave per token, the rows of W in turn.
 __global__ __launch_bounds__(256) void rowdot_kernel(const bf16_t *__restrict__ x, int T, int D,

@@ -120,6 +120,7 @@ struct DecodeJob {
     uint32_t *ids;    // [T, k] and
     bf16_t *scores;   // [T, k]: the routing, computed once by a top-k launch when T > 4
     int topk_in_kernel;  // T <= 4: each workgroup re-derives the top-k from the logits instead
+    int router_done;     // logits and sh_logit already computed (quantized router or gate)
     bf16_t *sh_logit; // [T]
     bf16_t *sh_act;   // [T, S]
     bf16_t *act;      // [T*k, I], pair p = t*k + j
@@ -178,5 +179,7 @@ hipError_t launch_rms_norm(const bf16_t *x, const bf16_t *res, const bf16_t *w, 
 hipError_t launch_rowdot(const bf16_t *x, int T, int D, const bf16_t *W, int N,
                          const bf16_t *bias, bf16_t *y, hipStream_t stream);
 hipError_t launch_add_bias(bf16_t *y, const bf16_t *bias, int rows, int n, hipStream_t stream);
+// dst[0..n) = v (a kernel, not a memset node, so that captured graphs replay it faithfully)
+hipError_t launch_fill_u32(uint32_t *dst, uint32_t v, int n, hipStream_t stream);
 
 }  // namespace mrun

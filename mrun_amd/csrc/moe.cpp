@@ -80,11 +80,16 @@ static Status check_quantized(const mrun_quantized *q, const std::string &path, 
         return Err(MRUN_ERR_INVALID, path + ": " + std::to_string(q->in / q->group_size) +
                                          " scale groups do not divide the input width " +
                                          std::to_string(q->in));
-    if (q->bits != 4)
-        return Err(MRUN_ERR_UNSUPPORTED,
-                   path + ": " + std::to_string(q->bits) + "-bit weights are not run by this build");
+    if (q->in % (128 / q->bits) != 0)
+        return Err(MRUN_ERR_UNSUPPORTED, path + ": input width " + std::to_string(q->in) +
+                                             " must be a multiple of " +
+                                             std::to_string(128 / q->bits));
     if (!aligned16(q->weight)) return Err(MRUN_ERR_INVALID, path + ": codes must be 16-byte aligned");
     return Ok();
+}
+
+static bool same_quant(const mrun_quantized &a, const mrun_quantized &b) {
+    return a.bits == b.bits && a.group_size == b.group_size;
 }
 
 static Status check_ptr(const void *p, const char *what) {
@@ -112,15 +117,17 @@ static Status check_block(const mrun_sparse_moe *m) {
     const mrun_moe_config &c = m->cfg;
     TRY(check_config(c));
     const int D = c.hidden, E = c.experts, I = c.intermediate, S = c.shared_intermediate;
-    // router: dense bf16 [E, D] (+ bias [E])
-    if (!m->gate.weight)
-        return Err(MRUN_ERR_UNSUPPORTED, "gate: quantized routers are not run by this build");
+    // router: dense bf16 or quantized [E, D] (+ bias [E])
     if (m->gate.out != E || m->gate.in != D)
         return Err(MRUN_ERR_INVALID, "gate: shape must be [experts, hidden]");
-    TRY(check_ptr(m->gate.weight, "gate.weight"));
+    if (m->gate.weight) TRY(check_ptr(m->gate.weight, "gate.weight"));
+    else TRY(check_quantized(&m->gate.q, "gate", 1, E, D));
     TRY(check_quantized(&m->switch_gate_proj, "switch_mlp.gate_proj", E, I, D));
     TRY(check_quantized(&m->switch_up_proj, "switch_mlp.up_proj", E, I, D));
     TRY(check_quantized(&m->switch_down_proj, "switch_mlp.down_proj", E, D, I));
+    if (!same_quant(m->switch_gate_proj, m->switch_up_proj))
+        return Err(MRUN_ERR_UNSUPPORTED,
+                   "switch_mlp.gate_proj and up_proj must share bits and group size");
     if (S > 0) {
         const mrun_linear *mlp[3] = {&m->shared_gate_proj, &m->shared_up_proj,
                                      &m->shared_down_proj};
@@ -136,12 +143,14 @@ static Status check_block(const mrun_sparse_moe *m) {
         TRY(check_quantized(&m->shared_gate_proj.q, names[0], 1, S, D));
         TRY(check_quantized(&m->shared_up_proj.q, names[1], 1, S, D));
         TRY(check_quantized(&m->shared_down_proj.q, names[2], 1, D, S));
-        if (!m->shared_expert_gate.weight)
+        if (!same_quant(m->shared_gate_proj.q, m->shared_up_proj.q))
             return Err(MRUN_ERR_UNSUPPORTED,
-                       "shared_expert_gate: quantized gates are not run by this build");
+                       "shared_expert.gate_proj and up_proj must share bits and group size");
         if (m->shared_expert_gate.out != 1 || m->shared_expert_gate.in != D)
             return Err(MRUN_ERR_INVALID, "shared_expert_gate: shape must be [1, hidden]");
-        TRY(check_ptr(m->shared_expert_gate.weight, "shared_expert_gate.weight"));
+        if (m->shared_expert_gate.weight)
+            TRY(check_ptr(m->shared_expert_gate.weight, "shared_expert_gate.weight"));
+        else TRY(check_quantized(&m->shared_expert_gate.q, "shared_expert_gate", 1, 1, D));
     }
     return Ok();
 }
@@ -240,8 +249,17 @@ static Status quantized_matmul(const bf16_t *x, int rows, const mrun_quantized &
     return Ok();
 }
 
-static Status linear(const bf16_t *x, int rows, const mrun_linear &l, bf16_t *y, hipStream_t s) {
-    if (l.weight) return linear_dense(x, rows, l, y, s);
+// Linear::forward (load.rs:294-306), dense or quantized. `zero` [n_zero] is cleared before the
+// product's results are visible to later launches (the prefill routing counters).
+static Status linear(const bf16_t *x, int rows, const mrun_linear &l, bf16_t *y, hipStream_t s,
+                     uint32_t *zero = nullptr, int n_zero = 0) {
+    if (l.weight) {
+        // the MFMA branch clears `zero` itself
+        const bool mfma = rows > 16 && !(l.out < 16) && l.in % 64 == 0;
+        if (zero && !mfma) TRY_HIP(launch_fill_u32(zero, 0u, n_zero, s), "clear");
+        return linear_dense(x, rows, l, y, s, mfma ? zero : nullptr, n_zero);
+    }
+    if (zero) TRY_HIP(launch_fill_u32(zero, 0u, n_zero, s), "clear");
     TRY(quantized_matmul(x, rows, l.q, y, s));
     if (l.bias) TRY_HIP(launch_add_bias(y, l.bias, rows, l.out, s), "linear bias");
     return Ok();
@@ -251,7 +269,7 @@ static Status linear(const bf16_t *x, int rows, const mrun_linear &l, bf16_t *y,
 static Status router(const mrun_sparse_moe &m, const bf16_t *x, int T, bf16_t *logits,
                      bf16_t *gates, uint32_t *ids, bf16_t *scores, hipStream_t s) {
     const mrun_moe_config &c = m.cfg;
-    TRY(linear_dense(x, T, m.gate, logits, s));
+    TRY(linear(x, T, m.gate, logits, s));
     TRY_HIP(launch_topk(logits, T, c.experts, c.top_k, c.norm_topk_prob != 0, gates, ids, scores,
                         s),
             "router top-k");
@@ -271,6 +289,17 @@ static const char *kPrefillStages =
 static bool is_decode(const mrun_moe_config &c, int T) {
     return decode_supported(c.hidden, c.intermediate, c.shared_intermediate, T, c.top_k,
                             c.experts);
+}
+
+// The decode kernels stream 4-bit experts; 8-bit ones take the generic products.
+static bool is_decode(const mrun_sparse_moe &m, int T) {
+    const mrun_moe_config &c = m.cfg;
+    bool four = m.switch_gate_proj.bits == 4 && m.switch_up_proj.bits == 4 &&
+                m.switch_down_proj.bits == 4;
+    if (c.shared_intermediate > 0)
+        four = four && m.shared_gate_proj.q.bits == 4 && m.shared_up_proj.q.bits == 4 &&
+               m.shared_down_proj.q.bits == 4;
+    return four && is_decode(c, T);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -310,7 +339,7 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
     bf16_t *sh_y = S ? (bf16_t *)at(p.sh_y) : nullptr;
     const int max_slots = E < P ? E : P;
 
-    const bool decode = is_decode(c, T);
+    const bool decode = is_decode(m, T);
     const bool mfma = D % 64 == 0 && I % 64 == 0 && (S == 0 || S % 64 == 0);  // K of each product
 
     if (decode) {
@@ -327,17 +356,22 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
         }
         j.logits = logits, j.sh_logit = sh_logit, j.sh_act = sh_act, j.act = act, j.out = out;
         j.ids = ids, j.scores = scores, j.topk_in_kernel = T <= 4;
+        // quantized router or shared gate (8-bit in mlx-community conversions): their logits come
+        // from the generic products, and the decode launches start at the routed experts
+        if (!m.gate.weight || (S && !m.shared_expert_gate.weight)) {
+            TRY(tensor::linear(x, T, m.gate, logits, s));
+            if (S) TRY(tensor::linear(x, T, m.shared_expert_gate, sh_logit, s));
+            j.router_done = 1;
+        }
         TRY_HIP(launch_decode(j, s, &st), "decode");
         return Ok();
     }
 
     // prefill
     uint32_t *counts = (uint32_t *)at(p.counts), *rank = (uint32_t *)at(p.rank);
-    const bool mfma_router = T > 16 && E >= 16 && D % 64 == 0;  // linear_dense's MFMA branch
-    if (!mfma_router) TRY_HIP(hipMemsetAsync(counts, 0, 4 * (size_t)E, s), "clear counts");
-    TRY(tensor::linear_dense(x, T, m.gate, logits, s, mfma_router ? counts : nullptr, E));
+    TRY(tensor::linear(x, T, m.gate, logits, s, counts, E));
     st.mark(s);
-    if (S) TRY(tensor::linear_dense(x, T, m.shared_expert_gate, sh_logit, s));
+    if (S) TRY(tensor::linear(x, T, m.shared_expert_gate, sh_logit, s));
     st.mark(s);
     TRY_HIP(launch_topk_rank(logits, T, E, k, c.norm_topk_prob != 0, ids, scores, counts, rank, s),
             "top-k");
@@ -472,6 +506,7 @@ int mrun_moe_forward_profiled(const mrun_sparse_moe *moe, const mrun_bf16 *x, in
 
 const char *mrun_moe_stage_names(const mrun_moe_config *cfg, int32_t tokens) {
     if (!cfg || tokens <= 0) return "";
+    // for 4-bit experts (8-bit ones run the prefill stages at every token count)
     return models::is_decode(*cfg, tokens) ? models::kDecodeStages : models::kPrefillStages;
 }
 

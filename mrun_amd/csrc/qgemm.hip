@@ -1,5 +1,5 @@
 // Prefill-shaped products on the matrix cores (gfx950 v_mfma_f32_32x32x16_bf16):
-//  - grouped 4-bit expert GEMM over expert-sorted row tiles (gather_qmm with sorted indices,
+//  - grouped 4- or 8-bit expert GEMM over expert-sorted row tiles (gather_qmm with sorted indices,
 //    nuvec.rs:670-686), optionally with the gate/up pair and SwiGLU fused in the epilogue
 //    (moe.rs:79-83, activations.rs:55-59);
 //  - dense bf16 GEMM (the router's Linear, load.rs:294-306).
@@ -31,6 +31,17 @@ __device__ __forceinline__ uint4 codes_to_pairs(uint32_t w) {
                       ((w >> 8) & 0x000F000Fu) | 0x43004300u, ((w >> 12) & 0x000F000Fu) | 0x43004300u);
 }
 
+// Four 8-bit codes of one word -> bf16 pairs (q0, q1), (q2, q3): integers below 256 are exact in
+// bf16, so the top half of their f32 conversion is their bf16.
+__device__ __forceinline__ uint2 codes8_to_pairs(uint32_t w) {
+    const uint32_t f0 = __float_as_uint((float)(w & 0xffu));
+    const uint32_t f1 = __float_as_uint((float)((w >> 8) & 0xffu));
+    const uint32_t f2 = __float_as_uint((float)((w >> 16) & 0xffu));
+    const uint32_t f3 = __float_as_uint((float)(w >> 24));
+    return make_uint2(__builtin_amdgcn_perm(f1, f0, 0x07060302u),
+                      __builtin_amdgcn_perm(f3, f2, 0x07060302u));
+}
+
 // Eight bf16 x_0..x_7 (one uint4) re-paired as (x_i, x_{i+4}).
 __device__ __forceinline__ uint4 pair8(const uint4 &a) {
     return make_uint4(__builtin_amdgcn_perm(a.z, a.x, 0x05040100u),
@@ -45,11 +56,17 @@ __device__ __forceinline__ float dot2_(uint32_t a, uint32_t b, float c) {
                                            __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-template <bool QUANT, bool GLU, int SUB>
+// QB: 0 = dense bf16 B, 4 or 8 = affine-quantized B with that many bits per code. 8-bit codes
+// convert to exact bf16 integers (no offset, A in natural order).
+template <int QB, bool GLU, int SUB>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
+    constexpr bool QUANT = QB != 0;
     constexpr int NP = GLU ? 2 : 1;
     constexpr int TPR = GLU ? 2 : 4;           // B threads per output row (quantized)
-    constexpr int WPT = 8 / TPR;               // code words per B thread per step
+    constexpr int WPS = BK * (QB ? QB : 4) / 32;  // code words of a row per K step
+    constexpr int WPT = WPS / TPR;             // code words per B thread per step
+    constexpr int EPW = QB ? 32 / QB : 8;      // codes per word
+    constexpr float OFF = QB == 4 ? 128.f : 0.f;  // code offset of the B values
     __shared__ __align__(16) bf16_t As[BM * LDK];
     __shared__ __align__(16) bf16_t Bs[NP * BN * LDK];
     __shared__ float Sc[NP][SUB][BN], Bi[NP][SUB][BN];
@@ -90,7 +107,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
     const uint32_t *bcodes = nullptr;
     const bf16_t *bdense = nullptr;
     const int brow = min(n0 + bn, j.N - 1);  // columns past N load a valid row, never stored
-    if (QUANT) bcodes = wq.codes + ((size_t)e * wq.out + brow) * (K >> 3) + bq * WPT;
+    if (QUANT) bcodes = wq.codes + ((size_t)e * wq.out + brow) * (size_t)(K / EPW) + bq * WPT;
     else bdense = j.bd + (size_t)brow * K + bq * 16;
     // scales: thread -> (p, sub, n)
     const bool sthread = QUANT && tid < NP * SUB * BN;
@@ -107,7 +124,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
         ra1 = ((const uint4 *)(aptr + k0))[1];
         if (QUANT) {
 #pragma unroll
-            for (int i = 0; i < WPT; ++i) rw[i] = bcodes[(k0 >> 3) + i];
+            for (int i = 0; i < WPT; ++i) rw[i] = bcodes[k0 / EPW + i];
             const int g = (k0 + ss * (BK / SUB)) / wsq.group;
             rs = wsq.scales[srow + g];
             rbias = wsq.biases ? (uint32_t)wsq.biases[srow + g] : 0u;
@@ -130,7 +147,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
         __syncthreads();
         // stage A (and its group sums) and B into LDS
         if (QUANT) {
-            const uint4 pa0 = pair8(ra0), pa1 = pair8(ra1);
+            const uint4 pa0 = QB == 4 ? pair8(ra0) : ra0, pa1 = QB == 4 ? pair8(ra1) : ra1;
             *(uint4 *)&As[ar * LDK + ak] = pa0;
             *(uint4 *)&As[ar * LDK + ak + 8] = pa1;
             const uint32_t av[8] = {pa0.x, pa0.y, pa0.z, pa0.w, pa1.x, pa1.y, pa1.z, pa1.w};
@@ -144,13 +161,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
             } else {
                 if ((tid & 1) == 0) Xs[(tid & 3) >> 1][ar] = xs;
             }
-            bf16_t *bdst = &Bs[(bp * BN + bn) * LDK + bq * WPT * 8];
+            bf16_t *bdst = &Bs[(bp * BN + bn) * LDK + bq * WPT * EPW];
 #pragma unroll
-            for (int i = 0; i < WPT; ++i) *(uint4 *)(bdst + 8 * i) = codes_to_pairs(rw[i]);
+            for (int i = 0; i < WPT; ++i) {
+                if (QB == 4) *(uint4 *)(bdst + 8 * i) = codes_to_pairs(rw[i]);
+                else *(uint2 *)(bdst + 4 * i) = codes8_to_pairs(rw[i]);
+            }
             if (sthread) {
                 const float sc = bf2f(rs);
                 Sc[sp][ss][sn] = sc;
-                Bi[sp][ss][sn] = bf2f(rbias) - 128.f * sc;
+                Bi[sp][ss][sn] = bf2f(rbias) - OFF * sc;
             }
         } else {
             *(uint4 *)&As[ar * LDK + ak] = ra0;
@@ -623,16 +643,28 @@ hipError_t launch_gemm(const GemmJob &j, hipStream_t stream) {
     if (tiles <= 0) return hipSuccess;
     dim3 grid(tiles, (j.N + BN - 1) / BN, j.has_routing ? kGemmTileM / BM : 1);
     if (!j.bd) {
-        const bool sub2 = j.w0.group == 32;
+        // the gate/up pair shares one quantization
+        if (j.glu && (j.w1.bits != j.w0.bits || j.w1.group != j.w0.group)) return hipErrorInvalidValue;
+        const bool sub2 = j.w0.group == 32, b8 = j.w0.bits == 8;
         if (j.glu) {
-            if (sub2) gemm_kernel<true, true, 2><<<grid, 256, 0, stream>>>(j);
-            else gemm_kernel<true, true, 1><<<grid, 256, 0, stream>>>(j);
+            if (b8) {
+                if (sub2) gemm_kernel<8, true, 2><<<grid, 256, 0, stream>>>(j);
+                else gemm_kernel<8, true, 1><<<grid, 256, 0, stream>>>(j);
+            } else {
+                if (sub2) gemm_kernel<4, true, 2><<<grid, 256, 0, stream>>>(j);
+                else gemm_kernel<4, true, 1><<<grid, 256, 0, stream>>>(j);
+            }
         } else {
-            if (sub2) gemm_kernel<true, false, 2><<<grid, 256, 0, stream>>>(j);
-            else gemm_kernel<true, false, 1><<<grid, 256, 0, stream>>>(j);
+            if (b8) {
+                if (sub2) gemm_kernel<8, false, 2><<<grid, 256, 0, stream>>>(j);
+                else gemm_kernel<8, false, 1><<<grid, 256, 0, stream>>>(j);
+            } else {
+                if (sub2) gemm_kernel<4, false, 2><<<grid, 256, 0, stream>>>(j);
+                else gemm_kernel<4, false, 1><<<grid, 256, 0, stream>>>(j);
+            }
         }
     } else {
-        gemm_kernel<false, false, 1><<<grid, 256, 0, stream>>>(j);
+        gemm_kernel<0, false, 1><<<grid, 256, 0, stream>>>(j);
     }
     return hipGetLastError();
 }

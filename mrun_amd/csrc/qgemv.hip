@@ -1,11 +1,11 @@
-// Decode-shaped gathered 4-bit products (gather_qmm at few rows, nuvec.rs:670-686) for the
+// Decode-shaped gathered 4- and 8-bit products (gather_qmm at few rows, nuvec.rs:670-686) for the
 // facade ops and the block's generic path.
 //
-// Layout: a weight row of K codes is K/8 u32 words; LPR lanes share a row, each lane owning
-// 32-code chunks (one 128-bit load) li, li+LPR, ...; a 32-code chunk always lies in one quant
-// group (32 | group). Per (row, pair) a lane computes scale*sum(x*q) + bias*sum(x) over its chunks
-// in f32, then the LPR lanes are summed by a fixed butterfly: the order depends on K only, never
-// on how many rows or pairs are in flight (rows of a batch keep their one-row bits).
+// Layout: a weight row of K codes is K*BITS/32 u32 words; LPR lanes share a row, each lane owning
+// 128-bit code chunks (32 codes at 4 bits, 16 at 8) li, li+LPR, ...; a chunk always lies in one
+// quant group (chunk codes | group). Per (row, pair) a lane computes scale*sum(x*q) + bias*sum(x)
+// over its chunks in f32, then the LPR lanes are summed by a fixed butterfly: the order depends on
+// K only, never on how many rows or pairs are in flight (rows of a batch keep their one-row bits).
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -46,10 +46,28 @@ __device__ __forceinline__ float dot32(const uint4 &q, const uint4 *xv) {
     return acc;
 }
 
-__device__ __forceinline__ float sum32(const uint4 *xv) {
-    float s = 0.f;
+// sum_i x[i] * q[i] over the 16 8-bit codes of a chunk (codes 4wi..4wi+3 in word wi, LSB first).
+__device__ __forceinline__ float dot16_8(const uint4 &q, const uint4 *xv) {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    float acc = 0.f;
 #pragma unroll
     for (int wi = 0; wi < 4; ++wi) {
+        const uint4 xx = xv[wi >> 1];
+        const uint32_t xa = (wi & 1) ? xx.z : xx.x, xb = (wi & 1) ? xx.w : xx.y;
+        acc += bf_lo(xa) * (float)(w[wi] & 0xffu);
+        acc += bf_hi(xa) * (float)((w[wi] >> 8) & 0xffu);
+        acc += bf_lo(xb) * (float)((w[wi] >> 16) & 0xffu);
+        acc += bf_hi(xb) * (float)(w[wi] >> 24);
+    }
+    return acc;
+}
+
+// sum of the x values of a chunk (XQ x 8 bf16)
+template <int XQ>
+__device__ __forceinline__ float sum_x(const uint4 *xv) {
+    float s = 0.f;
+#pragma unroll
+    for (int wi = 0; wi < XQ; ++wi) {
         s += bf_lo(xv[wi].x) + bf_hi(xv[wi].x);
         s += bf_lo(xv[wi].y) + bf_hi(xv[wi].y);
         s += bf_lo(xv[wi].z) + bf_hi(xv[wi].z);
@@ -58,12 +76,14 @@ __device__ __forceinline__ float sum32(const uint4 *xv) {
     return s;
 }
 
+template <int BITS>
 __device__ __forceinline__ Chunk load_chunk(const QW &w, int e, int row, int ch) {
+    constexpr int CPC = 128 / BITS;  // codes per chunk
     Chunk c;
     const size_t r = (size_t)e * w.out + row;
-    const int words = w.in >> 3, groups = w.in / w.group;
+    const int words = w.in * BITS / 32, groups = w.in / w.group;
     c.q = *(const uint4 *)(w.codes + r * words + (size_t)ch * 4);
-    const int g = (ch * 32) / w.group;
+    const int g = (ch * CPC) / w.group;
     c.s = bf2f(w.scales[r * groups + g]);
     c.b = w.biases ? bf2f(w.biases[r * groups + g]) : 0.f;
     return c;
@@ -71,8 +91,10 @@ __device__ __forceinline__ Chunk load_chunk(const QW &w, int e, int row, int ch)
 
 // ---------------------------------------------------------------------------------------------
 
-template <bool GLU, int LPR, int CPL, int RG, int PCH>
+template <bool GLU, int LPR, int CPL, int RG, int PCH, int BITS>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvJob j) {
+    constexpr int CPC = 128 / BITS;    // codes per 128-bit chunk
+    constexpr int XQ = CPC / 8;        // 128-bit activation loads per chunk
     constexpr int RPI = 64 / LPR;      // rows per load instruction
     constexpr int ROWS_W = RG * RPI;   // rows per wave
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -107,7 +129,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvJob j) {
         A = j.xA, lda = j.x_lda, a_map = nullptr, a_div = 1;
         w0 = j.xw0, w1 = j.xw1, o_map = nullptr, out = j.xout, ldo = j.x_ldo;
     }
-    const int n_ch = w0.in >> 5;
+    const int n_ch = w0.in / CPC;
     const int row_base = (blockIdx.x * 4 + wave) * ROWS_W;
 
     Chunk c0[RG][CPL], c1[RG][CPL];
@@ -118,8 +140,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvJob j) {
         for (int c = 0; c < CPL; ++c) {
             const int ch = li + c * LPR;
             if (row < w0.out && ch < n_ch) {
-                c0[g][c] = load_chunk(w0, e, row, ch);
-                if (GLU) c1[g][c] = load_chunk(w1, e, row, ch);
+                c0[g][c] = load_chunk<BITS>(w0, e, row, ch);
+                if (GLU) c1[g][c] = load_chunk<BITS>(w1, e, row, ch);
             } else {
                 c0[g][c] = Chunk{make_uint4(0, 0, 0, 0), 0.f, 0.f};
                 c1[g][c] = c0[g][c];
@@ -128,7 +150,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvJob j) {
     }
 
     for (int p0 = lo; p0 < hi; p0 += PCH) {
-        uint4 xv[PCH][CPL][4];
+        uint4 xv[PCH][CPL][XQ];
         float xs[PCH][CPL];
 #pragma unroll
         for (int pp = 0; pp < PCH; ++pp) {
@@ -138,13 +160,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvJob j) {
             for (int c = 0; c < CPL; ++c) {
                 const int ch = li + c * LPR;
                 if (arow >= 0 && ch < n_ch) {
-                    const uint4 *src = (const uint4 *)(A + (size_t)arow * lda + ch * 32);
+                    const uint4 *src = (const uint4 *)(A + (size_t)arow * lda + ch * CPC);
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) xv[pp][c][q] = src[q];
-                    xs[pp][c] = sum32(xv[pp][c]);
+                    for (int q = 0; q < XQ; ++q) xv[pp][c][q] = src[q];
+                    xs[pp][c] = sum_x<XQ>(xv[pp][c]);
                 } else {
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) xv[pp][c][q] = make_uint4(0, 0, 0, 0);
+                    for (int q = 0; q < XQ; ++q) xv[pp][c][q] = make_uint4(0, 0, 0, 0);
                     xs[pp][c] = 0.f;
                 }
             }
@@ -165,9 +187,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvJob j) {
                 float a0 = 0.f, a1 = 0.f;
 #pragma unroll
                 for (int c = 0; c < CPL; ++c) {
-                    a0 += c0[g][c].s * dot32(c0[g][c].q, xv[pp][c]) + c0[g][c].b * xs[pp][c];
-                    if (GLU)
-                        a1 += c1[g][c].s * dot32(c1[g][c].q, xv[pp][c]) + c1[g][c].b * xs[pp][c];
+                    const float d0 = BITS == 4 ? dot32(c0[g][c].q, xv[pp][c])
+                                               : dot16_8(c0[g][c].q, xv[pp][c]);
+                    a0 += c0[g][c].s * d0 + c0[g][c].b * xs[pp][c];
+                    if (GLU) {
+                        const float d1 = BITS == 4 ? dot32(c1[g][c].q, xv[pp][c])
+                                                   : dot16_8(c1[g][c].q, xv[pp][c]);
+                        a1 += c1[g][c].s * d1 + c1[g][c].b * xs[pp][c];
+                    }
                 }
                 a0 = group_sum<LPR>(a0);
                 if (GLU) a1 = group_sum<LPR>(a1);
@@ -188,7 +215,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvJob j) {
     }
 }
 
-template <bool GLU, int LPR, int CPL>
+template <bool GLU, int BITS, int LPR, int CPL>
 static void launch_gemv_t(const GemvJob &j, hipStream_t stream) {
     constexpr int RG = GLU ? 4 : 8;
     constexpr int RPI = 64 / LPR;
@@ -196,37 +223,54 @@ static void launch_gemv_t(const GemvJob &j, hipStream_t stream) {
     const int extra = j.x_rows > 0 ? (j.x_rows + kExtraRowsPerSlot - 1) / kExtraRowsPerSlot : 0;
     const int rows = (extra && j.xw0.out > j.w0.out) ? j.xw0.out : j.w0.out;
     dim3 grid((rows + ROWS_B - 1) / ROWS_B, j.max_slots + extra);
-    gemv_kernel<GLU, LPR, CPL, RG, 1><<<grid, 256, 0, stream>>>(j);
+    gemv_kernel<GLU, LPR, CPL, RG, 1, BITS><<<grid, 256, 0, stream>>>(j);
 }
 
-template <bool GLU>
-static hipError_t launch_gemv_glu(const GemvJob &j, hipStream_t stream) {
-    const int n_ch = j.w0.in >> 5;
+// lanes per row from the chunks per row (the routed and the extra weights share K's chunking)
+template <bool GLU, int BITS>
+static hipError_t launch_gemv_bits(const GemvJob &j, hipStream_t stream) {
+    const int n_ch = j.max_slots > 0 ? j.w0.in / (128 / BITS) : j.xw0.in / (128 / BITS);
     if (n_ch >= 64) {
         const int cpl = (n_ch + 63) / 64;
-        if (cpl == 1) launch_gemv_t<GLU, 64, 1>(j, stream);
-        else if (cpl == 2) launch_gemv_t<GLU, 64, 2>(j, stream);
-        else if (cpl == 3) launch_gemv_t<GLU, 64, 3>(j, stream);
-        else if (cpl == 4) launch_gemv_t<GLU, 64, 4>(j, stream);
+        if (cpl == 1) launch_gemv_t<GLU, BITS, 64, 1>(j, stream);
+        else if (cpl == 2) launch_gemv_t<GLU, BITS, 64, 2>(j, stream);
+        else if (cpl == 3) launch_gemv_t<GLU, BITS, 64, 3>(j, stream);
+        else if (cpl == 4) launch_gemv_t<GLU, BITS, 64, 4>(j, stream);
+        else if (BITS == 8 && cpl <= 8) launch_gemv_t<GLU, BITS, 64, 8>(j, stream);
         else return hipErrorInvalidValue;
     } else if (n_ch >= 32) {
-        launch_gemv_t<GLU, 32, 2>(j, stream);
+        launch_gemv_t<GLU, BITS, 32, 2>(j, stream);
     } else if (n_ch >= 16) {
-        launch_gemv_t<GLU, 16, 2>(j, stream);
+        launch_gemv_t<GLU, BITS, 16, 2>(j, stream);
     } else if (n_ch >= 8) {
-        launch_gemv_t<GLU, 8, 2>(j, stream);
+        launch_gemv_t<GLU, BITS, 8, 2>(j, stream);
     } else if (n_ch >= 4) {
-        launch_gemv_t<GLU, 4, 2>(j, stream);
+        launch_gemv_t<GLU, BITS, 4, 2>(j, stream);
     } else if (n_ch >= 2) {
-        launch_gemv_t<GLU, 2, 2>(j, stream);
+        launch_gemv_t<GLU, BITS, 2, 2>(j, stream);
     } else {
-        launch_gemv_t<GLU, 1, 1>(j, stream);
+        launch_gemv_t<GLU, BITS, 1, 1>(j, stream);
     }
     return hipGetLastError();
 }
 
+template <bool GLU>
+static hipError_t launch_gemv_one(const GemvJob &j, hipStream_t stream) {
+    const int bits = j.max_slots > 0 ? j.w0.bits : j.xw0.bits;
+    return bits == 8 ? launch_gemv_bits<GLU, 8>(j, stream) : launch_gemv_bits<GLU, 4>(j, stream);
+}
+
 hipError_t launch_gemv(const GemvJob &j, hipStream_t stream) {
-    return j.glu ? launch_gemv_glu<true>(j, stream) : launch_gemv_glu<false>(j, stream);
+    // routed and extra (shared) weights of different widths or bit counts go in two launches
+    const bool split = j.max_slots > 0 && j.x_rows > 0 &&
+                       (j.xw0.bits != j.w0.bits || j.xw0.in != j.w0.in);
+    if (!split) return j.glu ? launch_gemv_one<true>(j, stream) : launch_gemv_one<false>(j, stream);
+    GemvJob a = j, b = j;
+    a.x_rows = 0;
+    b.max_slots = 0;
+    hipError_t e = j.glu ? launch_gemv_one<true>(a, stream) : launch_gemv_one<false>(a, stream);
+    if (e != hipSuccess) return e;
+    return j.glu ? launch_gemv_one<true>(b, stream) : launch_gemv_one<false>(b, stream);
 }
 
 }  // namespace mrun

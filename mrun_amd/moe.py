@@ -76,8 +76,13 @@ def _dense_linear(w: torch.Tensor, bias: torch.Tensor | None = None) -> Linear:
     return Linear(_ptr(w).value, Quantized(), _ptr(bias).value, out, in_)
 
 
-def _q_linear(q: DeviceQTensor) -> Linear:
-    return Linear(None, q.c, None, q.out, q.in_)
+def _q_linear(q: DeviceQTensor, bias: torch.Tensor | None = None) -> Linear:
+    return Linear(None, q.c, _ptr(bias).value, q.out, q.in_)
+
+
+def _linear(w, bias: torch.Tensor | None = None) -> Linear:
+    """load::Linear (load.rs:246-306): a dense bf16 tensor or a quantized DeviceQTensor."""
+    return _q_linear(w, bias) if isinstance(w, DeviceQTensor) else _dense_linear(w, bias)
 
 
 class SparseMoe:
@@ -88,9 +93,12 @@ class SparseMoe:
         (torch tensors and DeviceQTensors, as device_block makes)."""
         s = hb.shape
         self.shape = s
+        self.device = torch.device(device)
         dev = lambda a: a if isinstance(a, torch.Tensor) else bf16_tensor(a, device)
         qdev = lambda q: q if isinstance(q, DeviceQTensor) else DeviceQTensor(q, device)
-        self.router = dev(hb.router)
+        # the router and the shared-expert gate are dense bf16 or quantized (QTensor)
+        lin = lambda a: qdev(a) if isinstance(a, (QTensor, DeviceQTensor)) else dev(a)
+        self.router = lin(hb.router)
         self.router_bias = dev(hb.router_bias) if hb.router_bias is not None else None
         self.gate_proj = qdev(hb.gate_proj)
         self.up_proj = qdev(hb.up_proj)
@@ -100,12 +108,12 @@ class SparseMoe:
             self.sh_gate_proj = qdev(hb.sh_gate_proj)
             self.sh_up_proj = qdev(hb.sh_up_proj)
             self.sh_down_proj = qdev(hb.sh_down_proj)
-            self.sh_expert_gate = dev(hb.sh_expert_gate)
+            self.sh_expert_gate = lin(hb.sh_expert_gate)
         self.cfg = MoeConfig(s.hidden, s.experts, s.top_k, s.intermediate, int(s.norm_topk),
                              s.shared)
         m = _SparseMoe()
         m.cfg = self.cfg
-        m.gate = _dense_linear(self.router, self.router_bias)
+        m.gate = _linear(self.router, self.router_bias)
         m.switch_gate_proj = self.gate_proj.c
         m.switch_up_proj = self.up_proj.c
         m.switch_down_proj = self.down_proj.c
@@ -113,7 +121,7 @@ class SparseMoe:
             m.shared_gate_proj = _q_linear(self.sh_gate_proj)
             m.shared_up_proj = _q_linear(self.sh_up_proj)
             m.shared_down_proj = _q_linear(self.sh_down_proj)
-            m.shared_expert_gate = _dense_linear(self.sh_expert_gate)
+            m.shared_expert_gate = _linear(self.sh_expert_gate)
         self.c = m
         check(_lib.load().mrun_moe_check(ctypes.byref(self.c)))
         self._ws = None
@@ -121,10 +129,12 @@ class SparseMoe:
     def tensors(self) -> list:
         """Every device tensor of the block's weights."""
         qs = [self.gate_proj, self.up_proj, self.down_proj]
-        ts = [self.router] + ([self.router_bias] if self.router_bias is not None else [])
+        ts = [self.router_bias] if self.router_bias is not None else []
+        lins = [self.router] + ([self.sh_expert_gate] if self.shared else [])
         if self.shared:
             qs += [self.sh_gate_proj, self.sh_up_proj, self.sh_down_proj]
-            ts.append(self.sh_expert_gate)
+        for l in lins:
+            (qs if isinstance(l, DeviceQTensor) else ts).append(l)
         for q in qs:
             ts += [q.codes, q.scales] + ([q.biases] if q.biases is not None else [])
         return ts
@@ -135,7 +145,7 @@ class SparseMoe:
     def workspace(self, tokens: int) -> torch.Tensor:
         need = self.workspace_bytes(tokens)
         if self._ws is None or self._ws.numel() < need:
-            self._ws = torch.empty(need, dtype=torch.uint8, device=self.router.device)
+            self._ws = torch.empty(need, dtype=torch.uint8, device=self.device)
         return self._ws
 
     def forward(self, x: torch.Tensor, out: torch.Tensor | None = None,
@@ -252,7 +262,7 @@ class MoeStack:
     def workspace(self, tokens: int) -> torch.Tensor:
         need = int(_lib.load().mrun_moe_stack_workspace_bytes(ctypes.byref(self.layers[0].cfg), tokens))
         if self._ws is None or self._ws.numel() < need:
-            self._ws = torch.empty(need, dtype=torch.uint8, device=self.layers[0].router.device)
+            self._ws = torch.empty(need, dtype=torch.uint8, device=self.layers[0].device)
         return self._ws
 
     def forward_(self, x: torch.Tensor, workspace: torch.Tensor | None = None, stream=None) -> torch.Tensor:
@@ -301,11 +311,12 @@ def quantized_matmul(x: torch.Tensor, w: DeviceQTensor, stream=None) -> torch.Te
     return out
 
 
-def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
+def linear(x: torch.Tensor, weight, bias: torch.Tensor | None = None,
            stream=None) -> torch.Tensor:
-    """Linear::forward with a dense bf16 weight [out, in] (load.rs:294-306)."""
-    lin = _dense_linear(weight, bias)
-    out = torch.empty(x.shape[0], weight.shape[0], dtype=torch.bfloat16, device=x.device)
+    """Linear::forward (load.rs:294-306) with a dense bf16 weight [out, in] or a quantized
+    DeviceQTensor (one expert)."""
+    lin = _linear(weight, bias)
+    out = torch.empty(x.shape[0], lin.out, dtype=torch.bfloat16, device=x.device)
     check(_lib.load().mrun_linear_forward(ctypes.byref(lin), _ptr(x), x.shape[0], _ptr(out),
                                           _stream(stream)))
     return out

@@ -73,7 +73,7 @@ class HostBlock:
     """The tensors of one SparseMoe (moe.rs:109-147) on the host."""
 
     shape: Shape
-    router: np.ndarray                 # [E, D] bf16
+    router: "np.ndarray | QTensor"     # [E, D] bf16, or quantized (8-bit in real checkpoints)
     router_bias: np.ndarray | None     # [E] bf16
     gate_proj: QTensor
     up_proj: QTensor
@@ -81,7 +81,7 @@ class HostBlock:
     sh_gate_proj: QTensor | None = None
     sh_up_proj: QTensor | None = None
     sh_down_proj: QTensor | None = None
-    sh_expert_gate: np.ndarray | None = None  # [1, D] bf16
+    sh_expert_gate: "np.ndarray | QTensor | None" = None  # [1, D] bf16 or quantized
     zipf_rank: np.ndarray | None = field(default=None, repr=False)
 
     @property
@@ -174,27 +174,71 @@ def qtensor(config: int, layer: int, codes_id: int, scales_id: int, experts: int
     )
 
 
+def qtensor8(config: int, layer: int, codes_id: int, scales_id: int, experts: int, out: int,
+             in_: int, group: int = 64) -> QTensor:
+    """An 8-bit stacked weight: codes uniform 0..255, scales bf16(|bf16(0.02 N)| / 127.5), biases
+    -128 * scale (exact), so each weight dequantises to scale * (q - 128)."""
+    c = codes(seed(config, layer, codes_id), experts * out * in_ // 4, bits=8)
+    n = experts * out * in_ // group
+    sc = f32_to_bf16(np.abs(bf16_to_f32(normal_bf16(seed(config, layer, scales_id), n, 0.02)))
+                     / np.float32(127.5))
+    bi = f32_to_bf16(np.float32(-128.0) * bf16_to_f32(sc))
+    return QTensor(codes=c.reshape(experts, out, in_ // 4), scales=sc.reshape(experts, out, -1),
+                   biases=bi.reshape(experts, out, -1), experts=experts, out=out, in_=in_,
+                   group=group, bits=8)
+
+
+def quantize(w: np.ndarray, bits: int, group: int) -> QTensor:
+    """Affine quantization of a bf16 matrix [out, in] (or [E, out, in]) per group: scale =
+    bf16((max - min) / (2^bits - 1)), bias = bf16(min), q = clip(round((w - bias) / scale)),
+    codes packed LSB first. The format of mlx-community checkpoints' 8-bit routers; the exact
+    rounding of the scale does not matter to the block, which reads the stored values."""
+    w3 = bf16_to_f32(w).astype(np.float64)
+    if w3.ndim == 2:
+        w3 = w3[None]
+    E, out, in_ = w3.shape
+    g = w3.reshape(E, out, in_ // group, group)
+    lo, hi = g.min(axis=-1), g.max(axis=-1)
+    levels = (1 << bits) - 1
+    sc = f32_to_bf16(np.maximum((hi - lo) / levels, 1e-8).astype(np.float32))
+    bi = f32_to_bf16(lo.astype(np.float32))
+    s64, b64 = bf16_to_f32(sc).astype(np.float64), bf16_to_f32(bi).astype(np.float64)
+    q = np.clip(np.rint((g - b64[..., None]) / s64[..., None]), 0, levels).astype(np.uint32)
+    q = q.reshape(E, out, in_)
+    per = 32 // bits
+    words = np.zeros((E, out, in_ // per), np.uint32)
+    for i in range(per):
+        words |= q[:, :, i::per] << np.uint32(bits * i)
+    return QTensor(codes=words, scales=sc, biases=bi, experts=E, out=out, in_=in_, group=group,
+                   bits=bits)
+
+
 def make_block(shape: Shape, config: int = CFG_DECODE, layer: int = 0,
-               zipf: bool = False) -> HostBlock:
+               zipf: bool = False, expert_bits: int = 4, gate_bits: int = 0) -> HostBlock:
+    """The seeded block of the BASELINE configs. expert_bits 8 draws 8-bit experts and shared
+    expert (qtensor8); gate_bits 8 (or 4) quantizes the router and the shared-expert gate with
+    group 64, as mlx-community conversions store them."""
     D, E, I, S, g = shape.hidden, shape.experts, shape.intermediate, shape.shared, shape.group
     router = normal_bf16(seed(config, layer, ROUTER_W), E * D, 0.02).reshape(E, D)
     rb, rank = (None, None)
     if zipf:
         rb, rank = zipf_bias(seed(config, layer, ROUTER_BIAS), E)
+    qt = qtensor8 if expert_bits == 8 else qtensor
     blk = HostBlock(
         shape=shape,
-        router=router,
+        router=quantize(router, gate_bits, 64) if gate_bits else router,
         router_bias=rb,
-        gate_proj=qtensor(config, layer, GATE_CODES, GATE_SCALES, E, I, D, g),
-        up_proj=qtensor(config, layer, UP_CODES, UP_SCALES, E, I, D, g),
-        down_proj=qtensor(config, layer, DOWN_CODES, DOWN_SCALES, E, D, I, g),
+        gate_proj=qt(config, layer, GATE_CODES, GATE_SCALES, E, I, D, g),
+        up_proj=qt(config, layer, UP_CODES, UP_SCALES, E, I, D, g),
+        down_proj=qt(config, layer, DOWN_CODES, DOWN_SCALES, E, D, I, g),
         zipf_rank=rank,
     )
     if S:
-        blk.sh_gate_proj = qtensor(config, layer, SH_GATE_CODES, SH_GATE_SCALES, 1, S, D, g)
-        blk.sh_up_proj = qtensor(config, layer, SH_UP_CODES, SH_UP_SCALES, 1, S, D, g)
-        blk.sh_down_proj = qtensor(config, layer, SH_DOWN_CODES, SH_DOWN_SCALES, 1, D, S, g)
-        blk.sh_expert_gate = normal_bf16(seed(config, layer, SH_EXPERT_GATE), D, 0.02).reshape(1, D)
+        blk.sh_gate_proj = qt(config, layer, SH_GATE_CODES, SH_GATE_SCALES, 1, S, D, g)
+        blk.sh_up_proj = qt(config, layer, SH_UP_CODES, SH_UP_SCALES, 1, S, D, g)
+        blk.sh_down_proj = qt(config, layer, SH_DOWN_CODES, SH_DOWN_SCALES, 1, D, S, g)
+        sg = normal_bf16(seed(config, layer, SH_EXPERT_GATE), D, 0.02).reshape(1, D)
+        blk.sh_expert_gate = quantize(sg, gate_bits, 64) if gate_bits else sg
     return blk
 
 

@@ -127,14 +127,20 @@ def qweight(q, keep: _Keep) -> OrcQ:
     return OrcQ(_p(c), _p(s), _p(b), q.experts, q.out, q.in_, q.group, q.bits)
 
 
+def linear_of(w, bias, out: int, in_: int, keep: _Keep) -> OrcLinear:
+    """A Linear over a dense bf16 array or a quantized weight (anything with `codes`)."""
+    if hasattr(w, "codes"):
+        return OrcLinear(None, qweight(w, keep), _p(bias), out, in_)
+    return OrcLinear(_p(keep(w, np.uint16)), OrcQ(), _p(bias), out, in_)
+
+
 def block(hb, keep: _Keep) -> OrcBlock:
     """An OrcBlock over the arrays of a synthetic HostBlock (duck-typed)."""
     s = hb.shape
     b = OrcBlock()
     b.cfg = OrcConfig(s.hidden, s.experts, s.top_k, s.intermediate, int(s.norm_topk), s.shared)
-    r = keep(hb.router, np.uint16)
     rb = keep(hb.router_bias, np.uint16) if hb.router_bias is not None else None
-    b.gate = OrcLinear(_p(r), OrcQ(), _p(rb), s.experts, s.hidden)
+    b.gate = linear_of(hb.router, rb, s.experts, s.hidden, keep)
     b.sw_gate = qweight(hb.gate_proj, keep)
     b.sw_up = qweight(hb.up_proj, keep)
     b.sw_down = qweight(hb.down_proj, keep)
@@ -142,8 +148,7 @@ def block(hb, keep: _Keep) -> OrcBlock:
         b.sh_gate = OrcLinear(None, qweight(hb.sh_gate_proj, keep), None, s.shared, s.hidden)
         b.sh_up = OrcLinear(None, qweight(hb.sh_up_proj, keep), None, s.shared, s.hidden)
         b.sh_down = OrcLinear(None, qweight(hb.sh_down_proj, keep), None, s.hidden, s.shared)
-        g = keep(hb.sh_expert_gate, np.uint16)
-        b.sh_expert_gate = OrcLinear(_p(g), OrcQ(), None, 1, s.hidden)
+        b.sh_expert_gate = linear_of(hb.sh_expert_gate, None, 1, s.hidden, keep)
     return b
 
 
@@ -216,13 +221,14 @@ def qmatmul(q, x: np.ndarray) -> np.ndarray:
     return y
 
 
-def linear(w: np.ndarray, x: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
+def linear(w, x: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
+    """Linear::forward over a dense bf16 [out, in] array or a quantized weight (expert 0)."""
     keep = _Keep()
-    w = keep(w, np.uint16)
     b = keep(bias, np.uint16) if bias is not None else None
     x = keep(x, np.uint16)
-    l = OrcLinear(_p(w), OrcQ(), _p(b), w.shape[0], w.shape[1])
-    y = np.empty((x.shape[0], w.shape[0]), dtype=np.uint16)
+    out, in_ = (w.out, w.in_) if hasattr(w, "codes") else w.shape
+    l = linear_of(w, b, out, in_, keep)
+    y = np.empty((x.shape[0], out), dtype=np.uint16)
     if lib().orc_linear_forward(ctypes.byref(l), _p(x), x.shape[0], _p(y)) != 0:
         raise ValueError("orc_linear_forward: invalid arguments")
     return y

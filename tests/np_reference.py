@@ -32,6 +32,11 @@ def dequant(q) -> np.ndarray:
     return codes * s + b
 
 
+def weight(w) -> np.ndarray:
+    """[out, in] float64 of a Linear's weight: dense bf16, or expert 0 of a quantized one."""
+    return dequant(w)[0] if hasattr(w, "codes") else F(w)
+
+
 def sigmoid(z):
     return 1.0 / (1.0 + np.exp(-z))
 
@@ -51,7 +56,7 @@ def forward(hb, x_bits: np.ndarray, ids: np.ndarray | None = None):
     s = hb.shape
     x = F(x_bits)
     T, k = x.shape[0], s.top_k
-    logits = R(x @ F(hb.router).T)
+    logits = R(x @ weight(hb.router).T)
     if hb.router_bias is not None:
         logits = R(logits + F(hb.router_bias))
     m = logits.max(axis=1, keepdims=True)
@@ -74,7 +79,7 @@ def forward(hb, x_bits: np.ndarray, ids: np.ndarray | None = None):
             y[t, j] = R(Wd[ex] @ act)
     routed = R((R(y * sc[:, :, None])).sum(axis=1))
     if s.shared:
-        gl = R(x @ F(hb.sh_expert_gate).T)[:, 0]
+        gl = R(x @ weight(hb.sh_expert_gate).T)[:, 0]
         sg = R(sigmoid(gl))
         g = R(x @ dequant(hb.sh_gate_proj)[0].T)
         u = R(x @ dequant(hb.sh_up_proj)[0].T)

@@ -67,16 +67,29 @@ def status(m):
 def test_valid_blocks_pass():
     assert status(block()) == (0, "")
     assert status(block(D=6144, E=160, I=2560, S=0)) == (0, "")
+    # 8-bit experts, groups 32 and 128, and the 8-bit group-64 router and shared gate of
+    # mlx-community conversions (load.rs:14-17)
+    E, D, I, S = 256, 2048, 512, 512
+    m8 = block(switch_gate_proj=q(E, I, D, bits=8, group=32), switch_up_proj=q(E, I, D, bits=8, group=32),
+               switch_down_proj=q(E, D, I, bits=8, group=128),
+               gate=Linear(None, q(1, E, D, bits=8), None, E, D),
+               shared_expert_gate=Linear(None, q(1, 1, D, bits=8), None, 1, D))
+    assert status(m8) == (0, "")
 
 
 @pytest.mark.parametrize("over,code,text", [
     ({"switch_gate_proj": q(256, 512, 2048, group=16)}, _lib.MRUN_ERR_INVALID, "group size 16"),
     ({"switch_gate_proj": q(256, 512, 2048, bits=3)}, _lib.MRUN_ERR_INVALID, "3 bits"),
-    ({"switch_gate_proj": q(256, 512, 2048, bits=8)}, _lib.MRUN_ERR_UNSUPPORTED, "8-bit"),
+    ({"switch_gate_proj": q(256, 512, 2048, bits=8)}, _lib.MRUN_ERR_UNSUPPORTED,
+     "gate_proj and up_proj must share"),
     ({"switch_down_proj": q(256, 512, 2048)}, _lib.MRUN_ERR_INVALID, "down_proj: shape"),
     ({"switch_up_proj": q(256, 512, 2048, ptr=FAKE + 4)}, _lib.MRUN_ERR_INVALID, "aligned"),
-    ({"gate": Linear(None, q(256, 256, 2048), None, 256, 2048)}, _lib.MRUN_ERR_UNSUPPORTED,
-     "quantized routers"),
+    ({"gate": Linear(None, q(1, 256, 2048, bits=8), None, 128, 2048)}, _lib.MRUN_ERR_INVALID,
+     "gate: shape"),
+    ({"gate": Linear(None, q(1, 128, 2048, bits=8), None, 256, 2048)}, _lib.MRUN_ERR_INVALID,
+     "gate: shape [1, 128, 2048], expected [1, 256, 2048]"),
+    ({"shared_expert_gate": Linear(None, q(1, 1, 2048, bits=8, group=48), None, 1, 2048)},
+     _lib.MRUN_ERR_INVALID, "group size 48"),
 ])
 def test_invalid_blocks_are_refused(over, code, text):
     rc, msg = status(block(**over))

@@ -355,3 +355,85 @@ def test_stack_matches_layer_loop_and_oracle(stack3, T):
         own = O.moe_stack(hosts, x_np, None, 1e-6)
         _log(f"oracle stack vs GPU: {stats(got, own)}")
     _log(f"stack of 3, T={T}: {s}")
+
+
+# ---------------------------------------------------------------------------------------------
+# 8-bit weights and quantized routers (mlx-community conversions: 8-bit group-64 router and shared
+# gate, load.rs:14-17 and the tiny fixtures' quantization config)
+
+Q8 = synth.Shape(hidden=2048, experts=64, top_k=8, intermediate=512, shared=512)
+
+
+@pytest.fixture(scope="module")
+def q8_blocks():
+    out = {}
+    for name, kw in {"experts8": dict(expert_bits=8), "gates8": dict(gate_bits=8),
+                     "both8": dict(expert_bits=8, gate_bits=8)}.items():
+        hb = synth.make_block(Q8, config=synth.CFG_DECODE, layer=5, **kw)
+        out[name] = (hb, M.SparseMoe(hb))
+    return out
+
+
+@pytest.mark.parametrize("kind", ["experts8", "gates8", "both8"])
+@pytest.mark.parametrize("T", [1, 3, 16, 40, 300])
+def test_8bit_weights_match_oracle(q8_blocks, kind, T):
+    """8-bit experts run the generic products (GEMV at T <= 16, MFMA GEMM above); an 8-bit router
+    and shared gate run before the decode launches (T <= 16) or as the prefill's first product."""
+    hb, dev = q8_blocks[kind]
+    x_np = synth.make_x(Q8, T, config=synth.CFG_DECODE, layer=100 + T)
+    run_block(hb, dev, x_np, f"{kind} T={T}")
+
+
+@pytest.mark.parametrize("group", [32, 128])
+def test_8bit_groups(group):
+    shape = synth.Shape(hidden=1024, experts=16, top_k=4, intermediate=256, shared=256, group=group)
+    hb = synth.make_block(shape, config=synth.CFG_PLUMBING, layer=group, expert_bits=8, gate_bits=8)
+    dev = M.SparseMoe(hb)
+    for T in (2, 70):
+        run_block(hb, dev, synth.make_x(shape, T, config=synth.CFG_PLUMBING, layer=T),
+                  f"8-bit group {group} T={T}")
+
+
+def test_quantized_linear_facade():
+    """Linear::forward with an 8-bit weight and a bias (load.rs:294-306): R(R(x Wq^T) + b)."""
+    w = synth.normal_bf16(synth.seed(9, 0, synth.ROUTER_W), 96 * 512, 0.02).reshape(96, 512)
+    q = synth.quantize(w, 8, 64)
+    b = synth.normal_bf16(synth.seed(9, 0, synth.ROUTER_BIAS), 96, 0.1)
+    dq = M.DeviceQTensor(q)
+    for T in (1, 7, 33):
+        x_np = synth.make_x(synth.Shape(512, 1, 1, 32), T, config=9, layer=T)
+        got = M.bf16_bits(M.linear(M.bf16_tensor(x_np), dq, M.bf16_tensor(b)))
+        ref = O.linear(q, x_np, b)
+        assert beyond_rounding(got, ref) == 0, stats(got, ref)
+
+
+@pytest.mark.parametrize("T", [4, 40])
+def test_stack_graph_replays_match_eager(stack3, T):
+    """The stack captured as one HIP graph (no memset nodes: counters are cleared by kernels):
+    every replay, with eager work in between, equals the eager result."""
+    _, st = stack3
+    x0 = M.bf16_tensor(synth.make_x(STACK, T, config=synth.CFG_STACK, layer=500 + T))
+    eager = st.forward_(x0.clone())
+    torch.cuda.synchronize()
+    x = x0.clone()
+    ws = st.workspace(T).clone()  # the graph's own workspace
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        x.copy_(x0)
+        st.forward_(x, ws, stream=s)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        x.copy_(x0)
+        st.forward_(x, ws, stream=s)
+    torch.cuda.synchronize()
+    want = M.bf16_bits(eager)
+    for r in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(M.bf16_bits(x), want), f"replay {r}"
+        other = st.forward_(x0.clone())  # eager work between replays
+        torch.cuda.synchronize()
+        assert np.array_equal(M.bf16_bits(other), want)

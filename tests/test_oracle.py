@@ -272,6 +272,36 @@ def test_block_matches_numpy_restatement(shape, T, zipf):
     assert s["max_abs"] < 2e-3, s
 
 
+@pytest.mark.parametrize("shape,T,expert_bits,gate_bits", [
+    (TINY, 24, 8, 0), (TINY, 3, 4, 8), (TINY, 17, 8, 8),
+    (synth.Shape(hidden=256, experts=16, top_k=4, intermediate=128, shared=128, group=128),
+     20, 8, 8),
+])
+def test_block_8bit_and_quantized_gates_match_numpy(shape, T, expert_bits, gate_bits):
+    """8-bit experts (LSB-first bytes, nuvec.rs:1173-1204) and 8-bit group-64 router and shared
+    gate (Linear::Quantized, load.rs:294-306), as mlx-community checkpoints store them."""
+    hb = synth.make_block(shape, config=11, expert_bits=expert_bits, gate_bits=gate_bits)
+    x = synth.make_x(shape, T, config=11)
+    out, tr = O.moe_forward(hb, x, trace=True)
+    ref, rtr = NP.forward(hb, x, ids=tr["ids"])
+    assert beyond_rounding(tr["logits"], rtr["logits"]) == 0
+    s = assert_close(out, ref, l1_rel=2e-4, what="oracle vs numpy (8-bit)")
+    assert s["max_abs"] < 2e-3, s
+
+
+def test_quantize_round_trip():
+    """synth.quantize: every weight within half a step of its dequantised value."""
+    w = synth.normal_bf16(synth.seed(1, 0, synth.ROUTER_W), 16 * 256, 0.02).reshape(16, 256)
+    for bits in (4, 8):
+        q = synth.quantize(w, bits, 64)
+        d = NP.dequant(q)[0]
+        step = np.repeat(bf16_to_f32(q.scales[0]).astype(np.float64), 64, axis=-1)
+        assert np.all(np.abs(d - bf16_to_f32(w)) <= 0.5 * step + 1e-6)
+        # LSB-first packing: the first code of a row is the low bits of its first word
+        assert (q.codes[0, 0, 0] & ((1 << bits) - 1)) == np.rint(
+            (bf16_to_f32(w[0, 0]) - bf16_to_f32(q.biases[0, 0, 0])) / bf16_to_f32(q.scales[0, 0, 0]))
+
+
 def test_sorted_and_unsorted_dispatch_agree():
     """The oracle's sorted path (T*k >= 64, moe.rs:63-75) gives each row its unsorted bits."""
     hb = synth.make_block(TINY, config=8)
