@@ -119,6 +119,21 @@ SIGNATURES = {
         [c_void_p, c_int32, c_void_p, c_float, c_void_p, c_int32, c_void_p, c_size_t, c_void_p],
     ),
     "mrun_moe_stack_workspace_bytes": (c_size_t, [POINTER(MoeConfig), c_int32]),
+    # include/mrun_load.h
+    "mrun_weights_open": (c_int32, [c_char_p, POINTER(c_void_p)]),
+    "mrun_weights_close": (None, [c_void_p]),
+    "mrun_weights_moe_config": (c_int32, [c_void_p, POINTER(MoeConfig), POINTER(c_float)]),
+    "mrun_weights_tensor_info": (
+        c_int32, [c_void_p, c_char_p, c_char_p, POINTER(c_int64), POINTER(c_int32)]
+    ),
+    "mrun_weights_remaining": (c_int32, [c_void_p]),
+    "mrun_weights_resolve_quant": (
+        c_int32, [c_void_p, c_char_p, c_int32, POINTER(c_int32), POINTER(c_int32)]
+    ),
+    "mrun_weights_load_moe": (
+        c_int32, [c_void_p, c_char_p, POINTER(MoeConfig), POINTER(SparseMoe)]
+    ),
+    "mrun_weights_load_bf16": (c_int32, [c_void_p, c_char_p, c_int64, POINTER(c_void_p)]),
 }
 
 

@@ -17,39 +17,19 @@
 
 #include "kernels.hpp"
 #include "mrun_moe.h"
+#include "status.hpp"
 
 namespace mrun {
 
 // ---------------------------------------------------------------------------------------------
-// Status: the facade's Result<_, Error(String)>
-
-struct Status {
-    int code = MRUN_OK;
-    std::string msg;
-    bool ok() const { return code == MRUN_OK; }
-};
-
-static Status Ok() { return Status{}; }
-static Status Err(int code, std::string msg) { return Status{code, std::move(msg)}; }
+// the thread's last error (status.hpp)
 
 static thread_local std::string g_last_error;
 
-static int report(const Status &s) {
+int report(const Status &s) {
     g_last_error = s.ok() ? std::string() : s.msg;
     return s.code;
 }
-
-static Status hip_status(hipError_t e, const char *what) {
-    if (e == hipSuccess) return Ok();
-    return Err(MRUN_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
-}
-
-#define TRY(expr)                         \
-    do {                                  \
-        Status _s = (expr);               \
-        if (!_s.ok()) return _s;          \
-    } while (0)
-#define TRY_HIP(expr, what) TRY(hip_status((expr), (what)))
 
 static bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 

@@ -30,11 +30,17 @@ def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
 
 def bf16_tensor(a: np.ndarray, device="cuda") -> torch.Tensor:
     """uint16 bf16 bits -> torch.bfloat16 on the device (bit-exact)."""
-    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).to(device)
+    a = np.ascontiguousarray(a)
+    if not a.flags.writeable:  # e.g. a view of a read-only file buffer
+        a = a.copy()
+    return torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).to(device)
 
 
 def u32_tensor(a: np.ndarray, device="cuda") -> torch.Tensor:
-    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to(device)
+    a = np.ascontiguousarray(a, dtype=np.uint32)
+    if not a.flags.writeable:
+        a = a.copy()
+    return torch.from_numpy(a.view(np.int32)).to(device)
 
 
 def bf16_bits(t: torch.Tensor) -> np.ndarray:
@@ -125,6 +131,25 @@ class SparseMoe:
         self.c = m
         check(_lib.load().mrun_moe_check(ctypes.byref(self.c)))
         self._ws = None
+
+    @classmethod
+    def from_view(cls, view: "_SparseMoe", owner=None, device="cuda") -> "SparseMoe":
+        """A block over device memory someone else owns (a loaded checkpoint: mrun_amd.load),
+        kept alive through `owner`."""
+        self = cls.__new__(cls)
+        c = view.cfg
+        self.shape = Shape(hidden=c.hidden, experts=c.experts, top_k=c.top_k,
+                           intermediate=c.intermediate, shared=c.shared_intermediate,
+                           norm_topk=bool(c.norm_topk_prob))
+        self.device = torch.device(device)
+        self.cfg = MoeConfig(c.hidden, c.experts, c.top_k, c.intermediate, c.norm_topk_prob,
+                             c.shared_intermediate)
+        self.c = view
+        self.shared = c.shared_intermediate > 0
+        self._owner = owner
+        self._ws = None
+        check(_lib.load().mrun_moe_check(ctypes.byref(self.c)))
+        return self
 
     def tensors(self) -> list:
         """Every device tensor of the block's weights."""
@@ -249,6 +274,8 @@ class MoeStack:
     """A stack of MoE layers with the RMSNorm + residual around each (qwen3_5_moe.rs:622-624)."""
 
     def __init__(self, layers: list, norm_w: list | None = None, eps: float = 1e-6):
+        """norm_w: per layer a bf16 [hidden] device tensor, a raw device address (int), or None
+        (weight 1)."""
         self.layers = layers
         self.eps = eps
         self.norm_w = norm_w
@@ -256,7 +283,8 @@ class MoeStack:
         self._arr = (_SparseMoe * n)(*[l.c for l in layers])
         self._nw = None
         if norm_w is not None:
-            self._nw = (ctypes.c_void_p * n)(*[_ptr(w).value if w is not None else None for w in norm_w])
+            ptr = lambda w: w if isinstance(w, int) else (_ptr(w).value if w is not None else None)
+            self._nw = (ctypes.c_void_p * n)(*[ptr(w) for w in norm_w])
         self._ws = None
 
     def workspace(self, tokens: int) -> torch.Tensor:

@@ -22,7 +22,7 @@ def declared(header: Path) -> list[str]:
 
 def test_every_declared_symbol_is_exported():
     lib = _lib.load()
-    names = declared(ROOT / "include" / "mrun_moe.h")
+    names = declared(ROOT / "include" / "mrun_moe.h") + declared(ROOT / "include" / "mrun_load.h")
     assert len(names) >= 15
     for n in names:
         assert hasattr(lib, n), n
