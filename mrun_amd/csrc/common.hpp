@@ -9,6 +9,15 @@ typedef uint16_t bf16_t;
 namespace mrun {
 
 // bf16 bits <-> f32. Rounding is to nearest even; NaN stays NaN (quiet).
+// Workgroup barrier that waits for this wave's LDS (and scalar) operations only: global loads
+// issued before it stay in flight. __syncthreads also waits for every outstanding vector memory
+// operation (vmcnt(0)), which turns loads issued several steps ahead into loads waited for at the
+// next barrier. The "memory" clobber keeps the compiler from moving memory accesses across it; the
+// compiler still waits for each prefetched register before its first use.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 __device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }

@@ -1,0 +1,121 @@
+// Dense bf16 Linear on the matrix cores for prefill-sized inputs: the router and the shared
+// expert's gate (Linear::forward with a dense weight, load.rs:294-306): y = R(x W^T), then
+// R(y + bias). Both products read the same x, so they run as one launch (the gate is one more
+// column block).
+//
+// Workgroup tile 64 rows x 64 columns, 4 waves of 32 x 32 (v_mfma_f32_32x32x16_bf16), K steps of
+// 64. The loop is latency-bound (a K step is 4 MFMAs per wave), so each thread keeps three K steps
+// of loads in flight in registers (a ring unrolled by three) and the LDS tiles are double-buffered:
+// one barrier per K step, which waits for LDS only, so the loads stay in flight across it.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace mrun {
+
+namespace {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+
+constexpr int DBM = 64, DBN = 64, DBK = 64, DLDK = DBK + 8;
+
+struct Stage {
+    uint4 a0, a1, b0, b1;
+};
+
+__global__ __launch_bounds__(256) void dense_gemm_kernel(DenseJob j) {
+    __shared__ __align__(16) bf16_t As[2][DBM * DLDK];
+    __shared__ __align__(16) bf16_t Bs[2][DBN * DLDK];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (j.zero && blockIdx.x == 0 && blockIdx.y == 0)
+        for (int i = tid; i < j.n_zero; i += 256) j.zero[i] = 0;
+
+    // column block -> weight (W0's blocks first, then W1's)
+    const int nb0 = (j.N0 + DBN - 1) / DBN;
+    const bool second = (int)blockIdx.y >= nb0;
+    const bf16_t *W = second ? j.W1 : j.W0;
+    const bf16_t *bias = second ? j.bias1 : j.bias0;
+    const int N = second ? j.N1 : j.N0;
+    bf16_t *out = second ? j.out1 : j.out0;
+    const int ldo = second ? j.ldo1 : j.ldo0;
+    const int n0 = (second ? (int)blockIdx.y - nb0 : (int)blockIdx.y) * DBN;
+    const int row0 = blockIdx.x * DBM;
+    const int mrows = min(DBM, j.M - row0);
+    const int K = j.K, nks = K / DBK;
+
+    // staging: row tid / 4, 16 elements from k = 16 (tid % 4); rows past the end load the last
+    // row (never stored)
+    const int sr = tid >> 2, sk = (tid & 3) * 16;
+    const bf16_t *ap = j.A + (size_t)(row0 + min(sr, mrows - 1)) * j.lda + sk;
+    const bf16_t *bp = W + (size_t)min(n0 + sr, N - 1) * K + sk;
+    // stages pass by value (a reference into them would put the ring in scratch)
+    auto load = [&](int ks) __attribute__((always_inline)) -> Stage {
+        const uint4 *pa = (const uint4 *)(ap + ks * DBK), *pb = (const uint4 *)(bp + ks * DBK);
+        return Stage{pa[0], pa[1], pb[0], pb[1]};
+    };
+    auto store = [&](int ks, Stage st) __attribute__((always_inline)) {
+        bf16_t *a = &As[ks & 1][sr * DLDK + sk], *b = &Bs[ks & 1][sr * DLDK + sk];
+        *(uint4 *)a = st.a0, *(uint4 *)(a + 8) = st.a1;
+        *(uint4 *)b = st.b0, *(uint4 *)(b + 8) = st.b1;
+    };
+
+    const int wm = wave >> 1, wn = wave & 1, fr = lane & 31, fk = (lane >> 5) * 8;
+    f32x16_t acc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+    auto compute = [&](int ks) __attribute__((always_inline)) {
+        const bf16_t *a = &As[ks & 1][(wm * 32 + fr) * DLDK + fk];
+        const bf16_t *b = &Bs[ks & 1][(wn * 32 + fr) * DLDK + fk];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(bf16x8_t, *(const uint4 *)(a + 16 * s)),
+                __builtin_bit_cast(bf16x8_t, *(const uint4 *)(b + 16 * s)), acc, 0, 0, 0);
+    };
+    // step ks: its loads (issued three steps earlier) go to LDS buffer ks & 1, the registers are
+    // refilled with step ks + 3, then the tile is multiplied
+    auto step = [&](int ks, Stage st) __attribute__((always_inline)) -> Stage {
+        store(ks, st);
+        lds_barrier();
+        const Stage nx = load(min(ks + 3, nks - 1));  // clamped: the tail reloads a valid step
+        compute(ks);
+        return nx;
+    };
+
+    Stage s0 = load(0), s1 = load(min(1, nks - 1)), s2 = load(min(2, nks - 1));
+    int ks = 0;
+    for (; ks + 3 <= nks; ks += 3) {
+        s0 = step(ks, s0);
+        s1 = step(ks + 1, s1);
+        s2 = step(ks + 2, s2);
+    }
+    if (ks < nks) s0 = step(ks, s0);
+    if (ks + 1 < nks) s1 = step(ks + 1, s1);
+
+    const int col = n0 + wn * 32 + fr;
+    const float bv = (bias && col < N) ? bf2f(bias[col]) : 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int r = wm * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        if (r < mrows && col < N) {
+            float v = rbf(acc[i]);
+            if (bias) v = rbf(v + bv);
+            out[(size_t)(row0 + r) * ldo + col] = (bf16_t)f2bf(v);
+        }
+    }
+}
+
+}  // namespace
+
+bool dense_gemm_supported(int M, int K) { return M > 16 && K % DBK == 0 && K >= DBK; }
+
+hipError_t launch_dense_gemm(const DenseJob &j, hipStream_t stream) {
+    if (!dense_gemm_supported(j.M, j.K) || j.N0 <= 0 || (j.W1 && j.N1 <= 0))
+        return hipErrorInvalidValue;
+    const int nb = (j.N0 + DBN - 1) / DBN + (j.W1 ? (j.N1 + DBN - 1) / DBN : 0);
+    dim3 grid((j.M + DBM - 1) / DBM, nb);
+    dense_gemm_kernel<<<grid, 256, 0, stream>>>(j);
+    return hipGetLastError();
+}
+
+}  // namespace mrun

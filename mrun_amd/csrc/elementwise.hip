@@ -37,7 +37,10 @@ hipError_t launch_swiglu(const bf16_t *g, const bf16_t *u, int64_t n, bf16_t *ou
     return hipGetLastError();
 }
 
-// One workgroup per (token, 2048-column slab); thread = 8 columns.
+// One workgroup per (token, 2048-column slab); thread = 8 columns. All k row indices, then all k
+// rows, are loaded before the first is used (the rows' loads overlap instead of following each
+// other); the sum stays in j order.
+template <int KMAX>
 __global__ __launch_bounds__(256) void combine_kernel(const bf16_t *__restrict__ y,
                                                       const uint32_t *__restrict__ inverse,
                                                       const bf16_t *__restrict__ scores, int T,
@@ -47,23 +50,37 @@ __global__ __launch_bounds__(256) void combine_kernel(const bf16_t *__restrict__
     const int t = blockIdx.x;
     const int d = (blockIdx.y * 256 + threadIdx.x) * 8;
     if (d >= D) return;
+    uint32_t row[KMAX];
+    uint32_t sraw[KMAX];
+#pragma unroll
+    for (int jj = 0; jj < KMAX; ++jj) {
+        const int p = t * k + min(jj, k - 1);
+        row[jj] = inverse ? inverse[p] : (uint32_t)p;
+        sraw[jj] = scores[p];
+    }
+    uint4 yv[KMAX];
+#pragma unroll
+    for (int jj = 0; jj < KMAX; ++jj) yv[jj] = *(const uint4 *)(y + (size_t)row[jj] * D + d);
+    const float sg = sh_y ? rbf(sigmoidf_(bf2f(sh_logit[t]))) : 0.f;
+    uint4 sv = make_uint4(0, 0, 0, 0);
+    if (sh_y) sv = *(const uint4 *)(sh_y + (size_t)t * D + d);
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-    for (int jj = 0; jj < k; ++jj) {
-        const int p = t * k + jj;
-        const size_t row = inverse ? inverse[p] : (uint32_t)p;
-        const float s = bf2f(scores[p]);
-        float yf[8];
-        unpack8(*(const uint4 *)(y + row * D + d), yf);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] += rbf(yf[i] * s);
+    for (int jj = 0; jj < KMAX; ++jj) {
+        if (jj < k) {
+            const float s = bf2f(sraw[jj]);
+            float yf[8];
+            unpack8(yv[jj], yf);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] += rbf(yf[i] * s);
+        }
     }
     uint32_t o[8];
     if (sh_y) {
-        const float sg = rbf(sigmoidf_(bf2f(sh_logit[t])));
         float sf[8];
-        unpack8(*(const uint4 *)(sh_y + (size_t)t * D + d), sf);
+        unpack8(sv, sf);
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[i] = f2bf(rbf(acc[i]) + rbf(sg * sf[i]));
     } else {
@@ -78,7 +95,8 @@ hipError_t launch_combine(const bf16_t *y, const uint32_t *inverse, const bf16_t
                           int k, int D, const bf16_t *sh_y, const bf16_t *sh_logit, bf16_t *out,
                           hipStream_t stream) {
     dim3 grid(T, (D + 2047) / 2048);
-    combine_kernel<<<grid, 256, 0, stream>>>(y, inverse, scores, T, k, D, sh_y, sh_logit, out);
+    if (k <= 8) combine_kernel<8><<<grid, 256, 0, stream>>>(y, inverse, scores, T, k, D, sh_y, sh_logit, out);
+    else combine_kernel<16><<<grid, 256, 0, stream>>>(y, inverse, scores, T, k, D, sh_y, sh_logit, out);
     return hipGetLastError();
 }
 

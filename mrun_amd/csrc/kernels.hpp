@@ -162,10 +162,31 @@ struct GemmJob {
     int has_shared;
 };
 hipError_t launch_gemm(const GemmJob &job, hipStream_t stream);
-// whether launch_gemm runs the 128-row kernel (4-bit, group 64 or 128), which also takes `sh`
+// whether launch_gemm runs the tuned kernel (4-bit, group 64), which also takes `sh`
 bool qgemm_supported(const GemmJob &job);
 constexpr int kGemmTileM = 64;  // rows per routed tile
+
 constexpr int kGemmTileN = 64;
+
+// Dense bf16 Linear for more than 16 rows on the MFMAs (dense.hip): out0 = R(A W0^T) then
+// R(. + bias0), and optionally out1 from W1 in the same launch (the shared expert's gate beside the
+// router). K % 64 == 0. Workgroup (0, 0) clears zero[0..n_zero) first.
+struct DenseJob {
+    const bf16_t *A;
+    int lda, M, K;
+    const bf16_t *W0, *bias0;
+    int N0;
+    bf16_t *out0;
+    int ldo0;
+    const bf16_t *W1, *bias1;  // W1 null: none
+    int N1;
+    bf16_t *out1;
+    int ldo1;
+    uint32_t *zero;
+    int n_zero;
+};
+bool dense_gemm_supported(int M, int K);
+hipError_t launch_dense_gemm(const DenseJob &job, hipStream_t stream);
 
 // ---- elementwise ----
 

@@ -192,6 +192,14 @@ static Status linear_dense(const bf16_t *x, int rows, const mrun_linear &l, bf16
                            hipStream_t s, uint32_t *zero = nullptr, int n_zero = 0) {
     const int N = l.out, K = l.in;
     if (K % 8 != 0) return Err(MRUN_ERR_UNSUPPORTED, "linear: input width must be a multiple of 8");
+    if (dense_gemm_supported(rows, K)) {
+        DenseJob j{};
+        j.A = x, j.lda = K, j.M = rows, j.K = K;
+        j.W0 = l.weight, j.bias0 = l.bias, j.N0 = N, j.out0 = y, j.ldo0 = N;
+        j.zero = zero, j.n_zero = n_zero;
+        TRY_HIP(launch_dense_gemm(j, s), "linear (mfma)");
+        return Ok();
+    }
     if (rows > 16 && N < 16) {
         TRY_HIP(launch_rowdot(x, rows, K, l.weight, N, l.bias, y, s), "linear (rowdot)");
         return Ok();
@@ -234,8 +242,8 @@ static Status quantized_matmul(const bf16_t *x, int rows, const mrun_quantized &
 static Status linear(const bf16_t *x, int rows, const mrun_linear &l, bf16_t *y, hipStream_t s,
                      uint32_t *zero = nullptr, int n_zero = 0) {
     if (l.weight) {
-        // the MFMA branch clears `zero` itself
-        const bool mfma = rows > 16 && !(l.out < 16) && l.in % 64 == 0;
+        // the MFMA branches clear `zero` themselves
+        const bool mfma = dense_gemm_supported(rows, l.in) || (rows > 16 && !(l.out < 16) && l.in % 64 == 0);
         if (zero && !mfma) TRY_HIP(launch_fill_u32(zero, 0u, n_zero, s), "clear");
         return linear_dense(x, rows, l, y, s, mfma ? zero : nullptr, n_zero);
     }
@@ -349,9 +357,23 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
 
     // prefill
     uint32_t *counts = (uint32_t *)at(p.counts), *rank = (uint32_t *)at(p.rank);
-    TRY(tensor::linear(x, T, m.gate, logits, s, counts, E));
-    st.mark(s);
-    if (S) TRY(tensor::linear(x, T, m.shared_expert_gate, sh_logit, s));
+    if (m.gate.weight && (!S || m.shared_expert_gate.weight) && dense_gemm_supported(T, D)) {
+        // router and shared gate: one launch over x
+        DenseJob dj{};
+        dj.A = x, dj.lda = D, dj.M = T, dj.K = D;
+        dj.W0 = m.gate.weight, dj.bias0 = m.gate.bias, dj.N0 = E, dj.out0 = logits, dj.ldo0 = E;
+        if (S) {
+            dj.W1 = m.shared_expert_gate.weight, dj.bias1 = m.shared_expert_gate.bias;
+            dj.N1 = 1, dj.out1 = sh_logit, dj.ldo1 = 1;
+        }
+        dj.zero = counts, dj.n_zero = E;
+        TRY_HIP(launch_dense_gemm(dj, s), "router (mfma)");
+        st.mark(s);  // (the shared gate's stage below stays empty: it ran in this launch)
+    } else {
+        TRY(tensor::linear(x, T, m.gate, logits, s, counts, E));
+        st.mark(s);
+        if (S) TRY(tensor::linear(x, T, m.shared_expert_gate, sh_logit, s));
+    }
     st.mark(s);
     TRY_HIP(launch_topk_rank(logits, T, E, k, c.norm_topk_prob != 0, ids, scores, counts, rank, s),
             "top-k");
@@ -634,6 +656,8 @@ int mrun_moe_combine(const mrun_bf16 *y, const uint32_t *inverse, const mrun_bf1
     Status st;
     if (tokens <= 0 || top_k <= 0 || hidden <= 0 || hidden % 8 != 0)
         st = Err(MRUN_ERR_INVALID, "combine: bad shape (hidden must be a multiple of 8)");
+    else if (top_k > 16)
+        st = Err(MRUN_ERR_UNSUPPORTED, "combine: top_k above 16");
     if (st.ok()) st = check_ptr(y, "y");
     if (st.ok() && !scores) st = Err(MRUN_ERR_INVALID, "scores is null");
     if (st.ok() && shared_y) st = check_ptr(shared_y, "shared_y");

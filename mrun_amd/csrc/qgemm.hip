@@ -248,7 +248,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
 //    assigned to MFMA slots so that lane half h, sub-step s holds code word 4h + s of the step;
 //    the A tile is written in the same order (k block w at position 16 (w % 4) + 8 (w / 4)).
 //  - One barrier per K step (A, codes, scales are double-buffered); loads run 2 K steps (A),
-//    one super-step (codes) and one chunk (scales) ahead.
+//    one super-step (codes) and one chunk (scales) ahead. The barrier waits for LDS operations
+//    only, so those loads stay in flight across it.
 //  - The VALU does one FMA per output element and K step (acc += s * P', P' the MFMA chain of the
 //    step started from zero); the affine bias  sum_k (b - 128 s) x_k = b X - 128 s X  is a small
 //    GEMM over the chunk, [rows x 6 C] x [6 C x cols], run on the MFMAs with X = sum_k x_k of a
@@ -260,8 +261,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
 //  - Optional shared tiles (a non-routed product of the same N, the shared expert) come first.
 
 constexpr int G_BNB = 256, G_KSC = 16;
-// tile rows = 64 WM (WM waves along M), codes staged per SS K steps, SBUF buffers of scales
-constexpr int G_WM = 1, G_SS = 2, G_SBUF = 1, G_BM = 64 * G_WM, G_THREADS = 256 * G_WM;
+// tile rows = 64 WM (WM = 1, or 2 with 128-row routed tiles), codes staged per G_SS K steps,
+// G_SBUF buffers of scales
+constexpr int G_SS = 2, G_SBUF = 1;
 
 struct GTile {
     const bf16_t *A;
@@ -356,8 +358,12 @@ __global__ __launch_bounds__(256 * WM, 2 / WM) void qgemm_kernel(GemmJob j) {
     const int cr = tid / CU, cu = tid % CU;
     const uint32_t coff0 = weight_row(cr) * (uint32_t)(K >> 1) + 16u * cu;
     const uint32_t coff1 = weight_row(cr + RPU) * (uint32_t)(K >> 1) + 16u * cu;
-    const uint32_t coff2 = weight_row(cr + 2 * RPU) * (uint32_t)(K >> 1) + 16u * cu;
-    const uint32_t coff3 = weight_row(cr + 3 * RPU) * (uint32_t)(K >> 1) + 16u * cu;
+    // NCU = 4 / WM units per thread cover the 256 B rows: unit i is B row cr + RPU i, whose weight is
+    // the gate (codes0) for rows below NCOLS and the up projection (codes1) above, under glu
+    constexpr int NCU = 4 / WM;
+    static_assert(CU == 4 && NCU * G_THREADS == G_BNB * CU, "code units must cover the B rows once");
+    const uint32_t coff2 = NCU > 2 ? weight_row(cr + 2 * RPU) * (uint32_t)(K >> 1) + 16u * cu : 0u;
+    const uint32_t coff3 = NCU > 2 ? weight_row(cr + 3 * RPU) * (uint32_t)(K >> 1) + 16u * cu : 0u;
     const int cdst = cr * CU + (cu ^ swz(cr));  // + RPU * CU i (swz(cr + RPU i) == swz(cr))
     // scales / biases of a chunk: units u = tid + G_THREADS i (i < 4 / WM): array u / 512, B row
     // (u / 2) % 256, 16-byte half u % 2; offsets are clamped inside the tensor (a partial last
@@ -386,9 +392,13 @@ __global__ __launch_bounds__(256 * WM, 2 / WM) void qgemm_kernel(GemmJob j) {
     auto load_codes = [&](int ss) __attribute__((always_inline)) {  // super-step ss (clamped by the caller)
         const uint32_t o = 32u * SS * (uint32_t)ss;
         rc0 = *(const uint4 *)((const char *)codes0 + coff0 + o);
-        rc1 = *(const uint4 *)((const char *)codes0 + coff1 + o);
-        rc2 = *(const uint4 *)((const char *)codes1 + coff2 + o);
-        rc3 = *(const uint4 *)((const char *)codes1 + coff3 + o);
+        if (NCU > 2) {  // rows cr, cr + 64 gate; cr + 128, cr + 192 up
+            rc1 = *(const uint4 *)((const char *)codes0 + coff1 + o);
+            rc2 = *(const uint4 *)((const char *)codes1 + coff2 + o);
+            rc3 = *(const uint4 *)((const char *)codes1 + coff3 + o);
+        } else {        // rows cr gate, cr + 128 up
+            rc1 = *(const uint4 *)((const char *)codes1 + coff1 + o);
+        }
     };
     auto load_scales = [&](int ch) __attribute__((always_inline)) {  // chunk ch (clamped by the caller)
         const uint32_t o = (uint32_t)(ch * G_KSC);
@@ -403,8 +413,10 @@ __global__ __launch_bounds__(256 * WM, 2 / WM) void qgemm_kernel(GemmJob j) {
         uint4 *d = &Bc[ss & 1][cdst];
         d[0] = rc0;
         d[RPU * CU] = rc1;
-        d[2 * RPU * CU] = rc2;
-        d[3 * RPU * CU] = rc3;
+        if (NCU > 2) {
+            d[2 * RPU * CU] = rc2;
+            d[3 * RPU * CU] = rc3;
+        }
     };
     auto store_scales = [&](int ch) __attribute__((always_inline)) {
         uint4 *d = (uint4 *)&Sb[ch % SBUF][0][0][0];
@@ -550,7 +562,7 @@ __global__ __launch_bounds__(256 * WM, 2 / WM) void qgemm_kernel(GemmJob j) {
     load_scales(min(1, nch - 1));
     stage_a(ra0, 0);
     load_a(2, ra0);
-    __syncthreads();
+    lds_barrier();
     // K step k: compute k, stage k + 1 from `next` (loaded two steps ago), refill `next` with k + 3
     auto step = [&](int k, bool super_end, ARegs &next) __attribute__((always_inline)) {
         if (active) compute(k);
@@ -559,7 +571,7 @@ __global__ __launch_bounds__(256 * WM, 2 / WM) void qgemm_kernel(GemmJob j) {
                 store_codes((k + 1) / SS);
                 load_codes(min((k + 1) / SS + 1, nss - 1));
                 if ((k + 1) % G_KSC == 0) {
-                    if (SBUF == 1) __syncthreads();  // every wave is done with the chunk's scales
+                    if (SBUF == 1) lds_barrier();  // every wave is done with the chunk's scales
                     store_scales((k + 1) / G_KSC);
                     load_scales(min((k + 1) / G_KSC + 1, nch - 1));
                 }
@@ -567,7 +579,7 @@ __global__ __launch_bounds__(256 * WM, 2 / WM) void qgemm_kernel(GemmJob j) {
             stage_a(next, k + 1);
         }
         load_a(min(k + 3, nks - 1), next);
-        __syncthreads();
+        lds_barrier();
     };
     for (int ks = 0; ks < nks; ks += 4) {
         step(ks, SS == 1, ra1);
@@ -624,17 +636,23 @@ bool qgemm_supported(const GemmJob &j) {
     return true;
 }
 
+// 64-row tiles (WM = 1). The kernel also builds with WM = 2 (128-row tiles of 512 threads, one
+// workgroup per CU); measured at T = 4096 (experts averaging 128 rows) that was 12 % slower, so the
+// launcher keeps WM = 1.
+constexpr int G_WM = 1;
+
 hipError_t launch_gemm(const GemmJob &j, hipStream_t stream) {
     if (qgemm_supported(j)) {
+        constexpr int bm = 64 * G_WM;
         const int ncols = j.glu ? G_BNB / 2 : G_BNB;
         const int nblk = (j.N + ncols - 1) / ncols;
-        const int s_tiles = j.has_shared ? (j.sh.M + G_BM - 1) / G_BM : 0;
-        const int r_tiles = j.has_routing ? j.max_tiles : (j.M + G_BM - 1) / G_BM;
+        const int s_tiles = j.has_shared ? (j.sh.M + bm - 1) / bm : 0;
+        const int r_tiles = j.has_routing ? j.max_tiles : (j.M + bm - 1) / bm;
         const int tiles8 = (s_tiles + r_tiles + 7) / 8 * 8;
         if (tiles8 == 0) return hipSuccess;
         const dim3 grid(tiles8 * nblk);
-        if (j.glu) qgemm_kernel<true, G_WM, G_SS, G_SBUF><<<grid, G_THREADS, 0, stream>>>(j);
-        else qgemm_kernel<false, G_WM, G_SS, G_SBUF><<<grid, G_THREADS, 0, stream>>>(j);
+        if (j.glu) qgemm_kernel<true, G_WM, G_SS, G_SBUF><<<grid, 256 * G_WM, 0, stream>>>(j);
+        else qgemm_kernel<false, G_WM, G_SS, G_SBUF><<<grid, 256 * G_WM, 0, stream>>>(j);
         return hipGetLastError();
     }
     if (j.has_shared) return hipErrorInvalidValue;  // only the kernel above takes shared tiles

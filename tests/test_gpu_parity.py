@@ -234,6 +234,16 @@ def test_block_prefill_zipf_2048():
     _log(f"zipf: hottest expert {counts.max()} pairs = {counts.max() / counts.mean():.1f}x mean")
 
 
+def test_block_prefill_4096():
+    """configs[3]'s prefill chunk, T = 4096 (experts average 128 rows; the shared expert rides in the
+    expert launches)."""
+    hb = synth.make_block(Q, config=synth.CFG_STACK, layer=0)
+    dev = M.SparseMoe(hb)
+    x_np = synth.make_x(Q, 4096, config=synth.CFG_STACK, layer=4096)
+    rows = np.random.default_rng(1).choice(4096, 192, replace=False)
+    run_block(hb, dev, x_np, "Q T=4096 (192 sampled rows)", check_rows=np.sort(rows))
+
+
 def test_rows_keep_their_one_row_bits(q_dev):
     """A decode batch of T <= 16 rows gives every row the bits of its one-row product
     (with_row_exact, nuvec.rs:256-265; lanes.rs:68-112)."""
