@@ -68,9 +68,12 @@ hipError_t launch_permute(const uint32_t *ids, int P, int k, int E, const Permut
                           hipStream_t stream);
 
 // Prefill routing in two launches over many workgroups: top-k + per-workgroup histograms that
-// reserve ranges in counts[E] (zero on entry) with one atomic per (workgroup, expert), then a
-// scatter that places every pair inside its expert's range. Rows of an expert are contiguous but
-// not in token order; every row's result is independent of its position.
+// reserve ranges in counts[kRankSlots][E] (zero on entry) with one atomic per (workgroup, expert),
+// workgroup w using slot w % kRankSlots (one per XCD under round-robin dispatch, so workgroups of
+// different XCDs do not contend for one counter); then a scatter that places every pair inside its
+// expert's range (slot ranges in slot order). Rows of an expert are contiguous but not in token
+// order; every row's result is independent of its position.
+constexpr int kRankSlots = 8;
 hipError_t launch_topk_rank(const bf16_t *logits, int T, int E, int k, bool norm, uint32_t *ids,
                             bf16_t *scores, uint32_t *counts, uint32_t *rank,
                             hipStream_t stream);

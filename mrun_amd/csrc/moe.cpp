@@ -169,7 +169,7 @@ static Plan make_plan(const mrun_moe_config &c, int T) {
     p.n_active = take(4);
     p.tiles = take(12 * (size_t)p.max_tiles);
     p.n_tiles = take(4);
-    p.counts = take(4 * E);
+    p.counts = take(4 * (size_t)kRankSlots * E);
     p.rank = take(4 * P);
     p.act = take(2 * P * I);
     p.y = take(2 * P * D);
@@ -366,11 +366,11 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
             dj.W1 = m.shared_expert_gate.weight, dj.bias1 = m.shared_expert_gate.bias;
             dj.N1 = 1, dj.out1 = sh_logit, dj.ldo1 = 1;
         }
-        dj.zero = counts, dj.n_zero = E;
+        dj.zero = counts, dj.n_zero = kRankSlots * E;
         TRY_HIP(launch_dense_gemm(dj, s), "router (mfma)");
         st.mark(s);  // (the shared gate's stage below stays empty: it ran in this launch)
     } else {
-        TRY(tensor::linear(x, T, m.gate, logits, s, counts, E));
+        TRY(tensor::linear(x, T, m.gate, logits, s, counts, kRankSlots * E));
         st.mark(s);
         if (S) TRY(tensor::linear(x, T, m.shared_expert_gate, sh_logit, s));
     }

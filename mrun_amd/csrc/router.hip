@@ -201,8 +201,9 @@ __global__ __launch_bounds__(256) void topk_rank_kernel(const bf16_t *__restrict
     const size_t p0 = (size_t)t0 * k;
     if ((int)threadIdx.x < np) lr[threadIdx.x] = atomicAdd(&hist[ids[p0 + threadIdx.x]], 1u);
     __syncthreads();
+    uint32_t *slot_counts = counts + (size_t)(blockIdx.x % kRankSlots) * E;
     for (int e = threadIdx.x; e < E; e += 256)
-        if (hist[e]) base[e] = atomicAdd(&counts[e], hist[e]);
+        if (hist[e]) base[e] = atomicAdd(&slot_counts[e], hist[e]);
     __syncthreads();
     if ((int)threadIdx.x < np) rank[p0 + threadIdx.x] = base[ids[p0 + threadIdx.x]] + lr[threadIdx.x];
 }
@@ -216,22 +217,35 @@ hipError_t launch_topk_rank(const bf16_t *logits, int T, int E, int k, bool norm
     return hipGetLastError();
 }
 
-// Every block scans the E counts (1 KiB) itself; block 0 also writes offsets, the active list
-// and the tile list.
+// Every block scans the E counts (kRankSlots x E words) itself; block 0 also writes offsets, the
+// active list and the tile list.
 __global__ __launch_bounds__(1024) void scatter_kernel(const uint32_t *__restrict__ ids,
                                                        const uint32_t *__restrict__ rank,
                                                        const uint32_t *__restrict__ counts, int P,
                                                        int k, int E, PermuteOut o) {
-    __shared__ uint32_t off[1025], tmp[32];
+    __shared__ uint32_t off[kRankSlots][1025], tmp[32];
     const int tid = threadIdx.x;
-    const uint32_t cnt = tid < E ? counts[tid] : 0u;
+    // expert e's slot ranges follow each other in slot order
+    uint32_t cnt = 0;
+    if (tid < E) {
+#pragma unroll
+        for (int sl = 0; sl < kRankSlots; ++sl) {
+            off[sl][tid] = cnt;
+            cnt += counts[(size_t)sl * E + tid];
+        }
+    }
     uint32_t total;
     const uint32_t ex = block_exclusive_scan<1024>(cnt, tmp, &total);
-    if (tid < E) off[tid] = ex;
+    if (tid < E) {
+#pragma unroll
+        for (int sl = 0; sl < kRankSlots; ++sl) off[sl][tid] += ex;
+    }
     __syncthreads();
     const int p = blockIdx.x * 1024 + tid;
     if (p < P) {
-        const uint32_t pos = off[ids[p]] + rank[p];
+        // pair p came from top-k workgroup p / (4 k): slot (p / (4 k)) % kRankSlots
+        const int sl = (p / (4 * kRankTokensPerWave * k)) % kRankSlots;
+        const uint32_t pos = off[sl][ids[p]] + rank[p];
         if (o.order) o.order[pos] = (uint32_t)p;
         if (o.inverse) o.inverse[p] = pos;
         if (o.token) o.token[pos] = (uint32_t)(p / k);
