@@ -255,12 +255,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
 //    GEMM over the chunk, [rows x 6 C] x [6 C x cols], run on the MFMAs with X = sum_k x_k of a
 //    step split into three bf16 (hi + mid + lo == X exactly) against b and -128 s (exact).
 //  - A wave whose 64 rows are all past the tile only stages.
-//  - Tile t and column block nb go to workgroup L with L % 8 == t % 8: the hardware deals
-//    workgroups to the 8 XCDs round-robin, so all column blocks of a tile share one XCD's L2 and
-//    read the tile's A rows from it.
+//  - The hardware deals workgroups to the 8 XCDs round-robin (workgroup L to XCD L % 8). Blocks
+//    of G_TG consecutive tiles go to one XCD, dispatched one after the other: the column blocks of a
+//    tile share that XCD's L2 for the tile's A rows, and consecutive tiles of one expert (its rows
+//    beyond the first tile) share it for the expert's weights.
 //  - Optional shared tiles (a non-routed product of the same N, the shared expert) come first.
 
-constexpr int G_BNB = 256, G_KSC = 16;
+constexpr int G_BNB = 256, G_KSC = 16, G_TG = 4;
 // tile rows = 64 WM (WM = 1, or 2 with 128-row routed tiles), codes staged per G_SS K steps,
 // G_SBUF buffers of scales
 constexpr int G_SS = 2, G_SBUF = 1;
@@ -302,8 +303,11 @@ __global__ __launch_bounds__(256 * WM, 2 / WM) void qgemm_kernel(GemmJob j) {
 
     constexpr int NCOLS = GLU ? G_BNB / 2 : G_BNB;
     const int nblk = (j.N + NCOLS - 1) / NCOLS;
-    const int L = blockIdx.x, slot = L >> 3;
-    const int t = 8 * (slot / nblk) + (L & 7), nb = slot % nblk;
+    // XCD x = L % 8 takes blocks of G_TG consecutive tiles (b % 8 == x); within a block, the G_TG
+    // tiles of column block 0 come first, then column block 1, ...
+    const int L = blockIdx.x, slot = L >> 3, xcd = L & 7;
+    const int r = slot % (G_TG * nblk);
+    const int t = G_TG * (8 * (slot / (G_TG * nblk)) + xcd) + r % G_TG, nb = r / G_TG;
     const int s_tiles = j.has_shared ? (j.sh.M + G_BM - 1) / G_BM : 0;
     const bool shared_tile = t < s_tiles;
     GTile g;
@@ -648,7 +652,7 @@ hipError_t launch_gemm(const GemmJob &j, hipStream_t stream) {
         const int nblk = (j.N + ncols - 1) / ncols;
         const int s_tiles = j.has_shared ? (j.sh.M + bm - 1) / bm : 0;
         const int r_tiles = j.has_routing ? j.max_tiles : (j.M + bm - 1) / bm;
-        const int tiles8 = (s_tiles + r_tiles + 7) / 8 * 8;
+        const int tiles8 = (s_tiles + r_tiles + 8 * G_TG - 1) / (8 * G_TG) * (8 * G_TG);
         if (tiles8 == 0) return hipSuccess;
         const dim3 grid(tiles8 * nblk);
         if (j.glu) qgemm_kernel<true, G_WM, G_SS, G_SBUF><<<grid, 256 * G_WM, 0, stream>>>(j);
