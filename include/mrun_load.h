@@ -54,8 +54,9 @@ int mrun_weights_resolve_quant(const mrun_weights *w, const char *path, int32_t 
  * cfg->shared_intermediate > 0, `<prefix>.shared_expert.*` and `<prefix>.shared_expert_gate`,
  * copies them to the device and fills `out`. Hugging Face layouts at `prefix` are restated first:
  * per-expert `experts.<e>.<proj>.weight` are stacked (qwen3_moe.rs:39-58) and a fused
- * `experts.gate_up_proj` is split into gate and up (qwen3_5_moe.rs:391-405). Dense (unquantized)
- * experts and dense weights other than bf16 are refused with MRUN_ERR_UNSUPPORTED. */
+ * `experts.gate_up_proj` is split into gate and up (qwen3_5_moe.rs:391-405). Dense bf16 experts
+ * become 16-bit stacked weights (gather_mm); dense weights other than bf16 (f32 checkpoints) are
+ * refused with MRUN_ERR_UNSUPPORTED. */
 int mrun_weights_load_moe(mrun_weights *w, const char *prefix, const mrun_moe_config *cfg,
                           mrun_sparse_moe *out);
 

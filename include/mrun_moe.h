@@ -43,7 +43,10 @@ enum {
 /* tensor::Quantized (nuvec.rs:602-638): affine codes, scales and biases with their group size and
  * bits. weight [experts, out, in*bits/32] u32, LSB-first codes (nuvec.rs:1199-1203); scales and
  * biases [experts, out, in/group_size] bf16; biases NULL means zeros (nuvec.rs:604, 616-619).
- * A non-stacked weight (quantized_matmul) has experts = 1. */
+ * A non-stacked weight (quantized_matmul) has experts = 1.
+ * bits = 16 carries unquantized experts (SwitchLinear::Dense, moe.rs:43-46, run by gather_mm,
+ * nuvec.rs:688-697): weight points to bf16 [experts, out, in], scales and biases are NULL and
+ * group_size is ignored. */
 typedef struct mrun_quantized {
     const uint32_t *weight;
     const mrun_bf16 *scales;

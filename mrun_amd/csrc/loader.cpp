@@ -577,10 +577,10 @@ static Status check_linear(const HostLinear &l, int experts, int out, int in, bo
     };
     if (l.bias && !allow_bias) return invalid("weights", l.path + ".bias is not supported");
     if (!l.quantized) {
-        if (stacked)
+        if (stacked && l.weight->dtype != "BF16")
             return Err(MRUN_ERR_UNSUPPORTED,
                        l.path + ": dense " + l.weight->dtype + " " + shape_str(l.weight->shape) +
-                           " experts (gather_mm) are not run by this build");
+                           " experts (gather_mm) are not run by this build (bf16 only)");
         if (l.weight->dtype != "BF16")
             return Err(MRUN_ERR_UNSUPPORTED, l.path + ": dense " + l.weight->dtype +
                                                  " weights are not run by this build (bf16 only)");
@@ -641,6 +641,11 @@ static Status to_device(mrun_weights &w, const HostLinear &l, int experts, int o
         v.experts = experts, v.out = out, v.in = in, v.group_size = l.q.group_size, v.bits = l.q.bits;
         if (q) *q = v;
         if (lin) lin->q = v;
+    } else if (q) {  // dense bf16 experts: a 16-bit stacked weight (gather_mm)
+        TRY(upload(w, *l.weight, &p));
+        mrun_quantized v{};
+        v.weight = (const uint32_t *)p, v.experts = experts, v.out = out, v.in = in, v.bits = 16;
+        *q = v;
     } else {
         TRY(upload(w, *l.weight, &p));
         lin->weight = (const mrun_bf16 *)p;
@@ -814,12 +819,8 @@ int mrun_weights_load_moe(mrun_weights *w, const char *prefix, const mrun_moe_co
         st = check_linear(sw[i], E, i == 2 ? D : I, i == 2 ? I : D, true, false);
     if (st.ok()) st = check_linear(gate, 1, E, D, false, true);
     if (st.ok() && S > 0) {
-        for (int i = 0; st.ok() && i < 3; ++i) {
+        for (int i = 0; st.ok() && i < 3; ++i)
             st = check_linear(sh[i], 1, i == 2 ? D : S, i == 2 ? S : D, false, false);
-            if (st.ok() && !sh[i].quantized)
-                st = Err(MRUN_ERR_UNSUPPORTED,
-                         sh[i].path + ": dense shared experts are not run by this build");
-        }
         if (st.ok()) st = check_linear(sh_gate, 1, 1, D, false, true);
     }
     mrun_sparse_moe m{};

@@ -42,6 +42,22 @@ static QW qw_of(const mrun_quantized &q) {
 
 static Status check_quantized(const mrun_quantized *q, const std::string &path, int experts,
                               int out, int in) {
+    if (q && q->bits == 16) {  // dense bf16 experts (SwitchLinear::Dense, moe.rs:43-46)
+        if (!q->weight) return Err(MRUN_ERR_INVALID, path + ": missing tensors");
+        if (q->scales || q->biases)
+            return Err(MRUN_ERR_INVALID, path + ": dense (16-bit) weights carry no scales or biases");
+        if (q->experts != experts || q->out != out || q->in != in)
+            return Err(MRUN_ERR_INVALID, path + ": shape [" + std::to_string(q->experts) + ", " +
+                                             std::to_string(q->out) + ", " + std::to_string(q->in) +
+                                             "], expected [" + std::to_string(experts) + ", " +
+                                             std::to_string(out) + ", " + std::to_string(in) + "]");
+        if (in % 8 != 0 || in > 4096)
+            return Err(MRUN_ERR_UNSUPPORTED,
+                       path + ": dense experts need an input width that is a multiple of 8, at "
+                              "most 4096");
+        if (!aligned16(q->weight)) return Err(MRUN_ERR_INVALID, path + ": weights must be 16-byte aligned");
+        return Ok();
+    }
     if (!q || !q->weight || !q->scales) return Err(MRUN_ERR_INVALID, path + ": missing tensors");
     if (q->experts != experts || q->out != out || q->in != in)
         return Err(MRUN_ERR_INVALID,
@@ -69,7 +85,15 @@ static Status check_quantized(const mrun_quantized *q, const std::string &path, 
 }
 
 static bool same_quant(const mrun_quantized &a, const mrun_quantized &b) {
-    return a.bits == b.bits && a.group_size == b.group_size;
+    return a.bits == b.bits && (a.bits == 16 || a.group_size == b.group_size);
+}
+
+// A Linear's weight as a stacked weight of one expert: quantized as is, dense bf16 as bits 16.
+static mrun_quantized as_quantized(const mrun_linear &l) {
+    if (!l.weight) return l.q;
+    mrun_quantized q{};
+    q.weight = (const uint32_t *)l.weight, q.experts = 1, q.out = l.out, q.in = l.in, q.bits = 16;
+    return q;
 }
 
 static Status check_ptr(const void *p, const char *what) {
@@ -113,17 +137,17 @@ static Status check_block(const mrun_sparse_moe *m) {
                                      &m->shared_down_proj};
         const char *names[3] = {"shared_expert.gate_proj", "shared_expert.up_proj",
                                 "shared_expert.down_proj"};
-        for (int i = 0; i < 3; ++i) {
-            if (mlp[i]->weight)
-                return Err(MRUN_ERR_UNSUPPORTED,
-                           std::string(names[i]) + ": dense shared experts are not run by this build");
+        for (int i = 0; i < 3; ++i)
             if (mlp[i]->bias)
                 return Err(MRUN_ERR_INVALID, std::string(names[i]) + ".bias is not supported");
-        }
-        TRY(check_quantized(&m->shared_gate_proj.q, names[0], 1, S, D));
-        TRY(check_quantized(&m->shared_up_proj.q, names[1], 1, S, D));
-        TRY(check_quantized(&m->shared_down_proj.q, names[2], 1, D, S));
-        if (!same_quant(m->shared_gate_proj.q, m->shared_up_proj.q))
+        // dense shared experts (a bf16 Linear) run as one 16-bit expert
+        const mrun_quantized sgq = as_quantized(m->shared_gate_proj),
+                             suq = as_quantized(m->shared_up_proj),
+                             sdq = as_quantized(m->shared_down_proj);
+        TRY(check_quantized(&sgq, names[0], 1, S, D));
+        TRY(check_quantized(&suq, names[1], 1, S, D));
+        TRY(check_quantized(&sdq, names[2], 1, D, S));
+        if (!same_quant(sgq, suq))
             return Err(MRUN_ERR_UNSUPPORTED,
                        "shared_expert.gate_proj and up_proj must share bits and group size");
         if (m->shared_expert_gate.out != 1 || m->shared_expert_gate.in != D)
@@ -285,8 +309,9 @@ static bool is_decode(const mrun_sparse_moe &m, int T) {
     bool four = m.switch_gate_proj.bits == 4 && m.switch_up_proj.bits == 4 &&
                 m.switch_down_proj.bits == 4;
     if (c.shared_intermediate > 0)
-        four = four && m.shared_gate_proj.q.bits == 4 && m.shared_up_proj.q.bits == 4 &&
-               m.shared_down_proj.q.bits == 4;
+        four = four && !m.shared_gate_proj.weight && !m.shared_up_proj.weight &&
+               !m.shared_down_proj.weight && m.shared_gate_proj.q.bits == 4 &&
+               m.shared_up_proj.q.bits == 4 && m.shared_down_proj.q.bits == 4;
     return four && is_decode(c, T);
 }
 
@@ -339,8 +364,8 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
         j.wd = qw_of(m.switch_down_proj);
         if (S) {
             j.sh_gate_w = m.shared_expert_gate.weight, j.sh_gate_b = m.shared_expert_gate.bias;
-            j.sg = qw_of(m.shared_gate_proj.q), j.su = qw_of(m.shared_up_proj.q);
-            j.sd = qw_of(m.shared_down_proj.q);
+            j.sg = qw_of(as_quantized(m.shared_gate_proj)), j.su = qw_of(as_quantized(m.shared_up_proj));
+            j.sd = qw_of(as_quantized(m.shared_down_proj));
         }
         j.logits = logits, j.sh_logit = sh_logit, j.sh_act = sh_act, j.act = act, j.out = out;
         j.ids = ids, j.scores = scores, j.topk_in_kernel = T <= 4;
@@ -396,10 +421,11 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
         GemmJob sg{}, sd{};
         if (S) {
             sg.A = x, sg.lda = D, sg.a_div = 1, sg.M = T, sg.N = S, sg.K = D;
-            sg.w0 = qw_of(m.shared_gate_proj.q), sg.w1 = qw_of(m.shared_up_proj.q);
+            sg.w0 = qw_of(as_quantized(m.shared_gate_proj));
+            sg.w1 = qw_of(as_quantized(m.shared_up_proj));
             sg.out = sh_act, sg.ldo = S, sg.glu = 1;
             sd.A = sh_act, sd.lda = S, sd.a_div = 1, sd.M = T, sd.N = D, sd.K = S;
-            sd.w0 = qw_of(m.shared_down_proj.q), sd.out = sh_y, sd.ldo = D;
+            sd.w0 = qw_of(as_quantized(m.shared_down_proj)), sd.out = sh_y, sd.ldo = D;
         }
         // the shared expert rides in the routed launches when its products have the same N
         bool fuse = S == I && qgemm_supported(g) && qgemm_supported(dn) && qgemm_supported(sg) &&
@@ -428,8 +454,8 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
         g.routing = rt, g.has_routing = 1, g.max_slots = max_slots;
         g.out = act, g.ldo = I, g.glu = 1;
         if (S) {
-            g.xA = x, g.x_lda = D, g.xw0 = qw_of(m.shared_gate_proj.q);
-            g.xw1 = qw_of(m.shared_up_proj.q), g.x_rows = T, g.xout = sh_act, g.x_ldo = S;
+            g.xA = x, g.x_lda = D, g.xw0 = qw_of(as_quantized(m.shared_gate_proj));
+            g.xw1 = qw_of(as_quantized(m.shared_up_proj)), g.x_rows = T, g.xout = sh_act, g.x_ldo = S;
         }
         TRY_HIP(launch_gemv(g, s), "gate/up (gemv)");
         st.mark(s);
@@ -437,7 +463,7 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
         dn.A = act, dn.lda = I, dn.a_div = 1, dn.w0 = qw_of(m.switch_down_proj);
         dn.routing = rt, dn.has_routing = 1, dn.max_slots = max_slots, dn.out = y, dn.ldo = D;
         if (S) {
-            dn.xA = sh_act, dn.x_lda = S, dn.xw0 = qw_of(m.shared_down_proj.q);
+            dn.xA = sh_act, dn.x_lda = S, dn.xw0 = qw_of(as_quantized(m.shared_down_proj));
             dn.x_rows = T, dn.xout = sh_y, dn.x_ldo = D;
         }
         TRY_HIP(launch_gemv(dn, s), "down (gemv)");

@@ -56,11 +56,14 @@ __device__ __forceinline__ float dot2_(uint32_t a, uint32_t b, float c) {
                                            __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-// QB: 0 = dense bf16 B, 4 or 8 = affine-quantized B with that many bits per code. 8-bit codes
-// convert to exact bf16 integers (no offset, A in natural order).
+// QB: 0 = dense bf16 B (j.bd, no experts), 4 or 8 = affine-quantized B with that many bits per
+// code, 16 = dense bf16 experts (QW with bits 16: gather_mm). 8-bit codes convert to exact bf16
+// integers (no offset, A in natural order).
 template <int QB, bool GLU, int SUB>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
-    constexpr bool QUANT = QB != 0;
+    constexpr bool QUANT = QB == 4 || QB == 8;
+    constexpr bool DEXP = QB == 16;
+    constexpr int NB4 = DEXP ? (GLU ? 4 : 2) : 2;  // 16-byte B loads per thread per step (dense)
     constexpr int NP = GLU ? 2 : 1;
     constexpr int TPR = GLU ? 2 : 4;           // B threads per output row (quantized)
     constexpr int WPS = BK * (QB ? QB : 4) / 32;  // code words of a row per K step
@@ -100,23 +103,24 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
     const bf16_t *aptr = j.A + (size_t)arow * j.lda + ak;
 
     // B
-    const int bp = QUANT ? tid / (BN * TPR) : 0;
-    const int bn = QUANT ? (tid % (BN * TPR)) / TPR : tid >> 2;
-    const int bq = QUANT ? tid % TPR : tid & 3;
+    const int bp = (QUANT || DEXP) ? tid / (BN * TPR) : 0;
+    const int bn = (QUANT || DEXP) ? (tid % (BN * TPR)) / TPR : tid >> 2;
+    const int bq = (QUANT || DEXP) ? tid % TPR : tid & 3;
     const QW &wq = (GLU && bp) ? j.w1 : j.w0;
     const uint32_t *bcodes = nullptr;
     const bf16_t *bdense = nullptr;
     const int brow = min(n0 + bn, j.N - 1);  // columns past N load a valid row, never stored
     if (QUANT) bcodes = wq.codes + ((size_t)e * wq.out + brow) * (size_t)(K / EPW) + bq * WPT;
+    else if (DEXP) bdense = (const bf16_t *)wq.codes + ((size_t)e * wq.out + brow) * K + bq * 8 * NB4;
     else bdense = j.bd + (size_t)brow * K + bq * 16;
     // scales: thread -> (p, sub, n)
     const bool sthread = QUANT && tid < NP * SUB * BN;
     const int sp = tid / (SUB * BN), ss = (tid / BN) % SUB, sn = tid % BN;
     const QW &wsq = (GLU && sp == 1) ? j.w1 : j.w0;
     const size_t srow =
-        ((size_t)e * wsq.out + min(n0 + sn, j.N - 1)) * (size_t)(K / wsq.group);
+        QUANT ? ((size_t)e * wsq.out + min(n0 + sn, j.N - 1)) * (size_t)(K / wsq.group) : 0;
 
-    uint4 ra0, ra1, rb0, rb1;
+    uint4 ra0, ra1, rb[NB4];
     uint32_t rw[WPT];
     uint32_t rs = 0, rbias = 0;  // raw bf16: converted when staged, a step after the load
     auto gload = [&](int k0) {
@@ -129,8 +133,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
             rs = wsq.scales[srow + g];
             rbias = wsq.biases ? (uint32_t)wsq.biases[srow + g] : 0u;
         } else {
-            rb0 = ((const uint4 *)(bdense + k0))[0];
-            rb1 = ((const uint4 *)(bdense + k0))[1];
+#pragma unroll
+            for (int i = 0; i < NB4; ++i) rb[i] = ((const uint4 *)(bdense + k0))[i];
         }
     };
 
@@ -175,8 +179,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
         } else {
             *(uint4 *)&As[ar * LDK + ak] = ra0;
             *(uint4 *)&As[ar * LDK + ak + 8] = ra1;
-            *(uint4 *)&Bs[bn * LDK + bq * 16] = rb0;
-            *(uint4 *)&Bs[bn * LDK + bq * 16 + 8] = rb1;
+            bf16_t *bdst = &Bs[(bp * BN + bn) * LDK + bq * 8 * NB4];
+#pragma unroll
+            for (int i = 0; i < NB4; ++i) *(uint4 *)(bdst + 8 * i) = rb[i];
         }
         __syncthreads();
         if (k0 + BK < K) gload(k0 + BK);
@@ -668,6 +673,11 @@ hipError_t launch_gemm(const GemmJob &j, hipStream_t stream) {
         // the gate/up pair shares one quantization
         if (j.glu && (j.w1.bits != j.w0.bits || j.w1.group != j.w0.group)) return hipErrorInvalidValue;
         const bool sub2 = j.w0.group == 32, b8 = j.w0.bits == 8;
+        if (j.w0.bits == 16) {
+            if (j.glu) gemm_kernel<16, true, 1><<<grid, 256, 0, stream>>>(j);
+            else gemm_kernel<16, false, 1><<<grid, 256, 0, stream>>>(j);
+            return hipGetLastError();
+        }
         if (j.glu) {
             if (b8) {
                 if (sub2) gemm_kernel<8, true, 2><<<grid, 256, 0, stream>>>(j);

@@ -1,5 +1,5 @@
-// Decode-shaped gathered 4- and 8-bit products (gather_qmm at few rows, nuvec.rs:670-686) for the
-// facade ops and the block's generic path.
+// Decode-shaped gathered 4- and 8-bit products (gather_qmm at few rows, nuvec.rs:670-686) and dense
+// bf16 ones (bits 16: gather_mm, nuvec.rs:688-697) for the facade ops and the block's generic path.
 //
 // Layout: a weight row of K codes is K*BITS/32 u32 words; LPR lanes share a row, each lane owning
 // 128-bit code chunks (32 codes at 4 bits, 16 at 8) li, li+LPR, ...; a chunk always lies in one
@@ -62,6 +62,17 @@ __device__ __forceinline__ float dot16_8(const uint4 &q, const uint4 *xv) {
     return acc;
 }
 
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_v;
+
+// sum_i x[i] * w[i] over the 8 dense bf16 weights of a chunk (f32 accumulation).
+__device__ __forceinline__ float dot8_16(const uint4 &q, const uint4 &x) {
+    auto d2 = [](uint32_t a, uint32_t b, float c) {
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a),
+                                               __builtin_bit_cast(bf16x2_v, b), c, false);
+    };
+    return d2(x.w, q.w, d2(x.z, q.z, d2(x.y, q.y, d2(x.x, q.x, 0.f))));
+}
+
 // sum of the x values of a chunk (XQ x 8 bf16)
 template <int XQ>
 __device__ __forceinline__ float sum_x(const uint4 *xv) {
@@ -81,8 +92,13 @@ __device__ __forceinline__ Chunk load_chunk(const QW &w, int e, int row, int ch)
     constexpr int CPC = 128 / BITS;  // codes per chunk
     Chunk c;
     const size_t r = (size_t)e * w.out + row;
-    const int words = w.in * BITS / 32, groups = w.in / w.group;
+    const int words = w.in * BITS / 32;
     c.q = *(const uint4 *)(w.codes + r * words + (size_t)ch * 4);
+    if (BITS == 16) {  // dense bf16: no affine map
+        c.s = 1.f, c.b = 0.f;
+        return c;
+    }
+    const int groups = w.in / w.group;
     const int g = (ch * CPC) / w.group;
     c.s = bf2f(w.scales[r * groups + g]);
     c.b = w.biases ? bf2f(w.biases[r * groups + g]) : 0.f;
@@ -163,7 +179,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvJob j) {
                     const uint4 *src = (const uint4 *)(A + (size_t)arow * lda + ch * CPC);
 #pragma unroll
                     for (int q = 0; q < XQ; ++q) xv[pp][c][q] = src[q];
-                    xs[pp][c] = sum_x<XQ>(xv[pp][c]);
+                    xs[pp][c] = BITS == 16 ? 0.f : sum_x<XQ>(xv[pp][c]);
                 } else {
 #pragma unroll
                     for (int q = 0; q < XQ; ++q) xv[pp][c][q] = make_uint4(0, 0, 0, 0);
@@ -187,6 +203,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvJob j) {
                 float a0 = 0.f, a1 = 0.f;
 #pragma unroll
                 for (int c = 0; c < CPL; ++c) {
+                    if (BITS == 16) {
+                        a0 += dot8_16(c0[g][c].q, xv[pp][c][0]);
+                        if (GLU) a1 += dot8_16(c1[g][c].q, xv[pp][c][0]);
+                        continue;
+                    }
                     const float d0 = BITS == 4 ? dot32(c0[g][c].q, xv[pp][c])
                                                : dot16_8(c0[g][c].q, xv[pp][c]);
                     a0 += c0[g][c].s * d0 + c0[g][c].b * xs[pp][c];
@@ -236,7 +257,7 @@ static hipError_t launch_gemv_bits(const GemvJob &j, hipStream_t stream) {
         else if (cpl == 2) launch_gemv_t<GLU, BITS, 64, 2>(j, stream);
         else if (cpl == 3) launch_gemv_t<GLU, BITS, 64, 3>(j, stream);
         else if (cpl == 4) launch_gemv_t<GLU, BITS, 64, 4>(j, stream);
-        else if (BITS == 8 && cpl <= 8) launch_gemv_t<GLU, BITS, 64, 8>(j, stream);
+        else if (BITS >= 8 && cpl <= 8) launch_gemv_t<GLU, BITS, 64, 8>(j, stream);
         else return hipErrorInvalidValue;
     } else if (n_ch >= 32) {
         launch_gemv_t<GLU, BITS, 32, 2>(j, stream);
@@ -257,6 +278,7 @@ static hipError_t launch_gemv_bits(const GemvJob &j, hipStream_t stream) {
 template <bool GLU>
 static hipError_t launch_gemv_one(const GemvJob &j, hipStream_t stream) {
     const int bits = j.max_slots > 0 ? j.w0.bits : j.xw0.bits;
+    if (bits == 16) return launch_gemv_bits<GLU, 16>(j, stream);
     return bits == 8 ? launch_gemv_bits<GLU, 8>(j, stream) : launch_gemv_bits<GLU, 4>(j, stream);
 }
 

@@ -59,7 +59,7 @@ class DeviceQTensor:
         if q is None:  # filled by from_tensors
             return
         self.codes = u32_tensor(q.codes, device)
-        self.scales = bf16_tensor(q.scales, device)
+        self.scales = bf16_tensor(q.scales, device) if q.scales is not None else None  # bits 16
         self.biases = bf16_tensor(q.biases, device) if q.biases is not None else None
         self.experts, self.out, self.in_, self.group, self.bits = q.experts, q.out, q.in_, q.group, q.bits
 

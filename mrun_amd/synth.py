@@ -51,10 +51,11 @@ CFG_PLUMBING, CFG_DECODE, CFG_PREFILL_ZIPF, CFG_STACK, CFG_CODER = 0, 1, 2, 3, 4
 
 @dataclass
 class QTensor:
-    """An affine 4-bit stacked weight: codes [E, out, in/8] u32, scales/biases [E, out, in/g]."""
+    """An affine 4/8-bit stacked weight: codes [E, out, in*bits/32] u32, scales/biases [E, out, in/g];
+    bits 16: dense bf16 weights in `codes` (two per word), no scales."""
 
     codes: np.ndarray
-    scales: np.ndarray
+    scales: np.ndarray | None
     biases: np.ndarray | None
     experts: int
     out: int
@@ -64,7 +65,7 @@ class QTensor:
 
     @property
     def nbytes(self) -> int:
-        b = self.codes.nbytes + self.scales.nbytes
+        b = self.codes.nbytes + (self.scales.nbytes if self.scales is not None else 0)
         return b + (self.biases.nbytes if self.biases is not None else 0)
 
 
@@ -188,6 +189,15 @@ def qtensor8(config: int, layer: int, codes_id: int, scales_id: int, experts: in
                    group=group, bits=8)
 
 
+def dense_experts(config: int, layer: int, codes_id: int, experts: int, out: int, in_: int,
+                  std: float = 0.02) -> QTensor:
+    """Unquantized bf16 expert weights N(0, std) [E, out, in] (SwitchLinear::Dense, moe.rs:43-46),
+    carried as bits 16: two bf16 per u32 word, the first in the low half; no scales."""
+    w = normal_bf16(seed(config, layer, codes_id), experts * out * in_, std)
+    return QTensor(codes=w.view(np.uint32).reshape(experts, out, in_ // 2), scales=None,
+                   biases=None, experts=experts, out=out, in_=in_, group=0, bits=16)
+
+
 def quantize(w: np.ndarray, bits: int, group: int) -> QTensor:
     """Affine quantization of a bf16 matrix [out, in] (or [E, out, in]) per group: scale =
     bf16((max - min) / (2^bits - 1)), bias = bf16(min), q = clip(round((w - bias) / scale)),
@@ -216,14 +226,17 @@ def quantize(w: np.ndarray, bits: int, group: int) -> QTensor:
 def make_block(shape: Shape, config: int = CFG_DECODE, layer: int = 0,
                zipf: bool = False, expert_bits: int = 4, gate_bits: int = 0) -> HostBlock:
     """The seeded block of the BASELINE configs. expert_bits 8 draws 8-bit experts and shared
-    expert (qtensor8); gate_bits 8 (or 4) quantizes the router and the shared-expert gate with
-    group 64, as mlx-community conversions store them."""
+    expert (qtensor8), 16 dense bf16 ones (dense_experts); gate_bits 8 (or 4) quantizes the router
+    and the shared-expert gate with group 64, as mlx-community conversions store them."""
     D, E, I, S, g = shape.hidden, shape.experts, shape.intermediate, shape.shared, shape.group
     router = normal_bf16(seed(config, layer, ROUTER_W), E * D, 0.02).reshape(E, D)
     rb, rank = (None, None)
     if zipf:
         rb, rank = zipf_bias(seed(config, layer, ROUTER_BIAS), E)
-    qt = qtensor8 if expert_bits == 8 else qtensor
+    if expert_bits == 16:
+        qt = lambda c, l, ci, si, e, o, i_, g_: dense_experts(c, l, ci, e, o, i_)
+    else:
+        qt = qtensor8 if expert_bits == 8 else qtensor
     blk = HostBlock(
         shape=shape,
         router=quantize(router, gate_bits, 64) if gate_bits else router,

@@ -50,7 +50,10 @@ int orc_set_threads(int32_t n) {
 /* ---- affine dequant (nuvec.rs:602-626, 1173-1204) ---- */
 
 static int qweight_ok(const orc_qweight *w) {
-    if (!w || !w->codes || !w->scales) return 0;
+    if (!w || !w->codes) return 0;
+    if (w->bits == 16)  /* dense bf16 (SwitchLinear::Dense): no scales */
+        return w->experts > 0 && w->out > 0 && w->in > 0 && w->in % 2 == 0;
+    if (!w->scales) return 0;
     if (w->bits != 4 && w->bits != 8) return 0;
     if (w->group <= 0 || w->in % w->group != 0) return 0;
     if ((w->in * w->bits) % 32 != 0) return 0;
@@ -58,6 +61,11 @@ static int qweight_ok(const orc_qweight *w) {
 }
 
 void orc_dequant_row(const orc_qweight *w, int32_t e, int32_t o, float *row) {
+    if (w->bits == 16) {  /* dense bf16 experts: the weight itself (gather_mm, nuvec.rs:688-697) */
+        const orc_bf16 *d = (const orc_bf16 *)w->codes + ((size_t)e * w->out + o) * (size_t)w->in;
+        for (int32_t i = 0; i < w->in; i++) row[i] = F(d[i]);
+        return;
+    }
     const int per = 32 / w->bits;
     const uint32_t mask = (1u << w->bits) - 1u;
     const size_t words = (size_t)w->in / per;

@@ -25,7 +25,8 @@
  * How each function is pinned (tests/test_oracle_*.py):
  *   orc_bf16_from_f32      torch's float32->bfloat16 conversion (RNE) on random and edge values
  *   orc_dequant_row        nuvec.rs:1173-1204 known answers (LSB-first nibbles, code*scale+bias,
- *                          zero biases); brute force on tiny shapes
+ *                          zero biases); brute force on tiny shapes; dense bf16 rows (bits 16)
+ *                          equal the stored weights
  *   orc_qmatmul / orc_gather_qmm   numpy float64 dequant+matmul (within f32 accumulation error),
  *                          the expert-selection closed form of nuvec.rs:1331-1357
  *   orc_linear             numpy float64 matmul + bias with the two roundings
@@ -55,7 +56,9 @@ extern "C" {
 typedef uint16_t orc_bf16;
 
 /* tensor::Quantized (nuvec.rs:602-626): codes [experts, out, in*bits/32], scales and biases
- * [experts, out, in/group]; biases NULL means zeros. */
+ * [experts, out, in/group]; biases NULL means zeros. bits == 16 holds dense bf16 weights
+ * [experts, out, in] in `codes` (SwitchLinear::Dense, moe.rs:43-46, run by gather_mm,
+ * nuvec.rs:688-697), with no scales. */
 typedef struct {
     const uint32_t *codes;
     const orc_bf16 *scales;

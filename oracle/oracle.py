@@ -122,7 +122,7 @@ class _Keep:
 def qweight(q, keep: _Keep) -> OrcQ:
     """Any object with codes/scales/biases arrays and experts/out/in_/group/bits."""
     c = keep(q.codes, np.uint32)
-    s = keep(q.scales, np.uint16)
+    s = keep(q.scales, np.uint16) if q.scales is not None else None
     b = keep(q.biases, np.uint16) if q.biases is not None else None
     return OrcQ(_p(c), _p(s), _p(b), q.experts, q.out, q.in_, q.group, q.bits)
 

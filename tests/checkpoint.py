@@ -72,3 +72,20 @@ def host_block(fixture: str, prefix: str) -> synth.HostBlock:
         hb.sh_down_proj = _q(t, prefix + ".shared_expert.down_proj", S)
         hb.sh_expert_gate = _q(t, prefix + ".shared_expert_gate", D)
     return hb
+
+
+def write(path: Path, tensors: dict, metadata: dict | None = None) -> None:
+    """Writes {name: numpy array (uint16 for bf16 bits, uint32 or float32)} as safetensors."""
+    dt = {np.dtype(np.uint16): "BF16", np.dtype(np.uint32): "U32", np.dtype(np.float32): "F32"}
+    header, chunks, at = {}, [], 0
+    if metadata:
+        header["__metadata__"] = metadata
+    for name in sorted(tensors):
+        a = np.ascontiguousarray(tensors[name])
+        b = a.tobytes()
+        header[name] = {"dtype": dt[a.dtype], "shape": list(a.shape), "data_offsets": [at, at + len(b)]}
+        chunks.append(b)
+        at += len(b)
+    h = json.dumps(header, separators=(",", ":")).encode()
+    h += b" " * (-len(h) % 8)
+    Path(path).write_bytes(struct.pack("<Q", len(h)) + h + b"".join(chunks))

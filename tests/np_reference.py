@@ -22,7 +22,10 @@ def F(bits) -> np.ndarray:
 
 
 def dequant(q) -> np.ndarray:
-    """[E, out, in] float64: code * scale + bias, codes LSB-first in each u32 word."""
+    """[E, out, in] float64: code * scale + bias, codes LSB-first in each u32 word; bits 16 holds
+    dense bf16 weights (two per word, the first in the low half)."""
+    if q.bits == 16:
+        return F(np.ascontiguousarray(q.codes).view(np.uint16).reshape(q.experts, q.out, q.in_))
     per = 32 // q.bits
     shifts = (np.arange(per, dtype=np.uint32) * q.bits)
     codes = (q.codes[..., None] >> shifts) & np.uint32((1 << q.bits) - 1)

@@ -75,6 +75,16 @@ def test_valid_blocks_pass():
                gate=Linear(None, q(1, E, D, bits=8), None, E, D),
                shared_expert_gate=Linear(None, q(1, 1, D, bits=8), None, 1, D))
     assert status(m8) == (0, "")
+    # dense bf16 experts (bits 16: SwitchLinear::Dense) and a dense bf16 shared expert
+    dn = lambda e, o, i: Quantized(FAKE, None, None, e, o, i, 0, 16)
+    md = block(switch_gate_proj=dn(E, I, D), switch_up_proj=dn(E, I, D), switch_down_proj=dn(E, D, I),
+               shared_gate_proj=Linear(FAKE, Quantized(), None, S, D),
+               shared_up_proj=Linear(FAKE, Quantized(), None, S, D),
+               shared_down_proj=Linear(FAKE, Quantized(), None, D, S))
+    assert status(md) == (0, "")
+    bad = block(switch_gate_proj=Quantized(FAKE, FAKE, None, E, I, D, 0, 16))
+    rc, msg = status(bad)
+    assert rc == _lib.MRUN_ERR_INVALID and "carry no scales" in msg, msg
 
 
 @pytest.mark.parametrize("over,code,text", [

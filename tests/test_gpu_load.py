@@ -72,3 +72,33 @@ def test_loaded_stack_with_norm_weights(T):
     assert np.all(np.abs(g - r) <= 2e-2 + bf16_ulp(np.maximum(np.abs(g), np.abs(r)))), s
     assert s["l1_rel"] <= 1e-3, s
     print(f"loaded stack T={T}: {s}", flush=True)
+
+
+@pytest.mark.parametrize("T", [2, 40])
+def test_hugging_face_layout_in_bf16(tmp_path, T):
+    """The Hugging Face fixture (fused gate_up_proj, dense experts, the model.language_model
+    prefix) with its f32 tensors rounded to bf16: the loader splits gate_up (qwen3_5_moe.rs:391-405)
+    and runs the dense experts; the oracle reads the same bf16 tensors split in numpy."""
+    src = C.read(C.GOLDEN / "tiny_qwen3_5_moe_hf" / "model.safetensors")
+    bf = {n: synth.f32_to_bf16(a.astype(np.float32)) for n, (dt, shp, a) in src.items() if dt == "F32"}
+    C.write(tmp_path / "model.safetensors", bf, {"format": "pt"})
+    (tmp_path / "config.json").write_text((C.GOLDEN / "tiny_qwen3_5_moe_hf" / "config.json").read_text())
+    p = "model.language_model.layers.0.mlp"
+    c = C.config("tiny_qwen3_5_moe_hf")
+    D, E, I, S = c["hidden_size"], c["num_experts"], c["moe_intermediate_size"], c["shared_expert_intermediate_size"]
+    gu = bf[p + ".experts.gate_up_proj"]                   # [E, 2I, D]
+    dense = lambda w: synth.QTensor(codes=np.ascontiguousarray(w).view(np.uint32), scales=None,
+                                    biases=None, experts=w.shape[0], out=w.shape[1], in_=w.shape[2],
+                                    group=0, bits=16)
+    shape = synth.Shape(hidden=D, experts=E, top_k=c["num_experts_per_tok"], intermediate=I, shared=S)
+    hb = synth.HostBlock(shape=shape, router=bf[p + ".gate.weight"], router_bias=None,
+                         gate_proj=dense(gu[:, :I, :]), up_proj=dense(gu[:, I:, :]),
+                         down_proj=dense(bf[p + ".experts.down_proj"]))
+    hb.sh_gate_proj = dense(bf[p + ".shared_expert.gate_proj.weight"][None])
+    hb.sh_up_proj = dense(bf[p + ".shared_expert.up_proj.weight"][None])
+    hb.sh_down_proj = dense(bf[p + ".shared_expert.down_proj.weight"][None])
+    hb.sh_expert_gate = bf[p + ".shared_expert_gate.weight"]
+    with Weights(tmp_path) as w:
+        dev = w.load_moe(p)
+        run_block(hb, dev, synth.make_x(shape, T, config=15, layer=T), f"HF bf16 T={T}")
+        torch.cuda.synchronize()

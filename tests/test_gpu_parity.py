@@ -447,3 +447,19 @@ def test_stack_graph_replays_match_eager(stack3, T):
         other = st.forward_(x0.clone())  # eager work between replays
         torch.cuda.synchronize()
         assert np.array_equal(M.bf16_bits(other), want)
+
+
+# ---------------------------------------------------------------------------------------------
+# dense bf16 experts (SwitchLinear::Dense, moe.rs:43-46 -> gather_mm, nuvec.rs:688-697)
+
+@pytest.fixture(scope="module")
+def dense_block():
+    hb = synth.make_block(Q8, config=synth.CFG_DECODE, layer=6, expert_bits=16)
+    return hb, M.SparseMoe(hb)
+
+
+@pytest.mark.parametrize("T", [1, 3, 16, 40, 300])
+def test_dense_experts_match_oracle(dense_block, T):
+    """Unquantized bf16 experts and shared expert (bits 16) on the generic GEMV and MFMA GEMM."""
+    hb, dev = dense_block
+    run_block(hb, dev, synth.make_x(Q8, T, config=synth.CFG_DECODE, layer=200 + T), f"dense T={T}")

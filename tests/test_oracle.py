@@ -273,13 +273,14 @@ def test_block_matches_numpy_restatement(shape, T, zipf):
 
 
 @pytest.mark.parametrize("shape,T,expert_bits,gate_bits", [
-    (TINY, 24, 8, 0), (TINY, 3, 4, 8), (TINY, 17, 8, 8),
+    (TINY, 24, 8, 0), (TINY, 3, 4, 8), (TINY, 17, 8, 8), (TINY, 12, 16, 0), (TINY, 20, 16, 8),
     (synth.Shape(hidden=256, experts=16, top_k=4, intermediate=128, shared=128, group=128),
      20, 8, 8),
 ])
 def test_block_8bit_and_quantized_gates_match_numpy(shape, T, expert_bits, gate_bits):
-    """8-bit experts (LSB-first bytes, nuvec.rs:1173-1204) and 8-bit group-64 router and shared
-    gate (Linear::Quantized, load.rs:294-306), as mlx-community checkpoints store them."""
+    """8-bit experts (LSB-first bytes, nuvec.rs:1173-1204), dense bf16 experts (bits 16,
+    SwitchLinear::Dense moe.rs:43-46) and 8-bit group-64 router and shared gate
+    (Linear::Quantized, load.rs:294-306), as mlx-community checkpoints store them."""
     hb = synth.make_block(shape, config=11, expert_bits=expert_bits, gate_bits=gate_bits)
     x = synth.make_x(shape, T, config=11)
     out, tr = O.moe_forward(hb, x, trace=True)
