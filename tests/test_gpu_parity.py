@@ -463,3 +463,36 @@ def test_dense_experts_match_oracle(dense_block, T):
     """Unquantized bf16 experts and shared expert (bits 16) on the generic GEMV and MFMA GEMM."""
     hb, dev = dense_block
     run_block(hb, dev, synth.make_x(Q8, T, config=synth.CFG_DECODE, layer=200 + T), f"dense T={T}")
+
+
+# ---------------------------------------------------------------------------------------------
+# edges of the configuration space (qwen3_5_moe.rs:508-513: 1 <= k <= E)
+
+@pytest.mark.parametrize("shape,Ts", [
+    # top-1 routing: one pair per token
+    (synth.Shape(hidden=2048, experts=64, top_k=1, intermediate=512, shared=512), (1, 16, 100)),
+    # 512 experts (eight per lane in the top-k) with k = 16, the widest top-k; T = 8 is the
+    # decode schedule's limit of 128 pairs, T = 9 the first prefill size
+    (synth.Shape(hidden=2048, experts=512, top_k=16, intermediate=256, shared=0), (1, 8, 9, 70)),
+    # k = E: every expert chosen by every token; norm_topk off
+    (synth.Shape(hidden=512, experts=8, top_k=8, intermediate=128, shared=128, norm_topk=False),
+     (1, 5, 40)),
+    # hidden not a multiple of 64 (the MFMA paths need K % 64 == 0; group 32): GEMV at every size
+    (synth.Shape(hidden=2080, experts=32, top_k=4, intermediate=544, shared=0, group=32), (2, 33)),
+])
+def test_config_edges(shape, Ts):
+    hb = synth.make_block(shape, config=synth.CFG_PLUMBING, layer=shape.experts + shape.top_k)
+    dev = M.SparseMoe(hb)
+    for T in Ts:
+        run_block(hb, dev, synth.make_x(shape, T, config=synth.CFG_PLUMBING, layer=300 + T),
+                  f"{shape.name} T={T}")
+
+
+def test_decode_boundary_t17(q_host, q_dev):
+    """T = 16 is the last decode size and T = 17 the first prefill one: the same token's output
+    agrees between them within the bar (the two schedules accumulate in different orders)."""
+    x17 = synth.make_x(Q, 17, config=synth.CFG_DECODE, layer=17)
+    a = M.bf16_bits(q_dev.forward(M.bf16_tensor(x17)))
+    b = M.bf16_bits(q_dev.forward(M.bf16_tensor(x17[:16])))
+    torch.cuda.synchronize()
+    assert_close(b, a[:16], what="T=16 decode vs T=17 prefill rows")
