@@ -112,4 +112,44 @@ __device__ __forceinline__ void unpack8(const uint4 &v, float *f) {
     f[6] = bf_lo(v.w); f[7] = bf_hi(v.w);
 }
 
+// ss + f[0]^2 + ... + f[7]^2 in that order, and 1 / sqrt(sum / D + eps): the two steps every
+// RMSNorm here shares, so that all of them round alike.
+__device__ __forceinline__ float sumsq8(const float *f, float ss) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) ss += f[k] * f[k];
+    return ss;
+}
+__device__ __forceinline__ float rms_inv_of(float sum, int D, float eps) {
+    return 1.0f / sqrtf(sum / (float)D + eps);
+}
+
+// 1 / sqrt(mean(x^2) + eps) of one bf16 row of D elements (D % 8 == 0), computed by one wave in a
+// fixed order — lane l sums elements 8 l + 512 i + j (i, then j) over 2048-element passes, then a
+// butterfly over the wave — so every kernel that normalises a row gets the same bits (RMSNorm,
+// fast::rms_norm nuvec.rs:796-798). With res, the row is R(x + res) (add_rms_norm).
+__device__ __forceinline__ float row_rms_inv(const bf16_t *x, const bf16_t *res, int D, float eps,
+                                             int lane) {
+    float ss = 0.f;
+    for (int d = lane * 8; d < D; d += 2048) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (d + 512 * i < D) {
+                const uint4 v = *(const uint4 *)(x + d + 512 * i);
+                float f[8];
+                f[0] = bf_lo(v.x), f[1] = bf_hi(v.x), f[2] = bf_lo(v.y), f[3] = bf_hi(v.y);
+                f[4] = bf_lo(v.z), f[5] = bf_hi(v.z), f[6] = bf_lo(v.w), f[7] = bf_hi(v.w);
+                if (res) {
+                    const uint4 r = *(const uint4 *)(res + d + 512 * i);
+                    f[0] = rbf(f[0] + bf_lo(r.x)), f[1] = rbf(f[1] + bf_hi(r.x));
+                    f[2] = rbf(f[2] + bf_lo(r.y)), f[3] = rbf(f[3] + bf_hi(r.y));
+                    f[4] = rbf(f[4] + bf_lo(r.z)), f[5] = rbf(f[5] + bf_hi(r.z));
+                    f[6] = rbf(f[6] + bf_lo(r.w)), f[7] = rbf(f[7] + bf_hi(r.w));
+                }
+                ss = sumsq8(f, ss);
+            }
+        }
+    }
+    return rms_inv_of(group_sum<64>(ss), D, eps);
+}
+
 }  // namespace mrun

@@ -87,20 +87,50 @@ __device__ __forceinline__ void gemv_wave(const QW &w0, const QW &w1, int e, int
     }
 }
 
+// Eight bf16 of a raw row through the RMSNorm: R(R(x * inv) * w), w eight bf16 (or ones).
+__device__ __forceinline__ uint4 norm8(uint4 x, float inv, uint4 w) {
+    const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, ws[4] = {w.x, w.y, w.z, w.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t ww = ws[k];
+        const uint32_t lo = f2bf(rbf(bf_lo(xs[k]) * inv) * bf_lo(ww));
+        const uint32_t hi = f2bf(rbf(bf_hi(xs[k]) * inv) * bf_hi(ww));
+        o[k] = lo | (hi << 16);
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// A lane's four 8-element pieces of a 2048-element pass of a row: elements [d + 512 i, +8),
+// clamped to the row's last 8 (the clamped pieces are never used).
+struct Row4 {
+    uint4 v[4];
+};
+__device__ __forceinline__ Row4 load_row4(const bf16_t *p, int d, int D) {
+    Row4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.v[i] = *(const uint4 *)(p + min(d + 512 * i, D - 8));
+    return r;
+}
+
 // One dense row for T <= 16 tokens (one wave): R(x[t] . w) then R(. + bias). Lane l owns
-// elements [8l + 512i, +8); tokens go in groups of 4 whose loads are issued together.
+// elements [8l + 512i, +8); tokens go in groups of 4 whose loads are issued together. `first` is
+// the lane's first pass of w (load_row4(w, 8 lane, D)), loaded by the caller as early as it can;
+// each later pass of w is loaded before the current one is used.
 template <int MAXT>
 __device__ __forceinline__ void router_row(const bf16_t *x, int T, int D, const bf16_t *w,
-                                           const bf16_t *bias, bf16_t *out, int ldo, int lane) {
+                                           Row4 first, const bf16_t *bias, bf16_t *out, int ldo,
+                                           int lane) {
     constexpr int TG = 4;
     float acc[MAXT];
 #pragma unroll
     for (int t = 0; t < MAXT; ++t) acc[t] = 0.f;
     const uint32_t braw = bias ? (uint32_t)*bias : 0u;
+    Row4 cur = first;
     for (int d = lane * 8; d < D; d += 2048) {
-        uint4 wv[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) wv[i] = *(const uint4 *)(w + min(d + 512 * i, D - 8));
+        const Row4 wr = cur;
+        if (d + 2048 < D) cur = load_row4(w, d + 2048, D);
+        const uint4 *wv = wr.v;
 #pragma unroll
         for (int t0 = 0; t0 < MAXT; t0 += TG) {
             if (t0 < T) {
@@ -148,7 +178,9 @@ __global__ __launch_bounds__(256) void rows_kernel(const bf16_t *__restrict__ x,
                                                    bf16_t *__restrict__ out) {
     const int lane = threadIdx.x & 63, r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= N) return;
-    router_row<MAXT>(x, T, D, W + (size_t)r * D, bias ? bias + r : nullptr, out + r, N, lane);
+    const bf16_t *w = W + (size_t)r * D;
+    router_row<MAXT>(x, T, D, w, load_row4(w, lane * 8, D), bias ? bias + r : nullptr, out + r, N,
+                     lane);
 }
 
 hipError_t launch_rows(const bf16_t *x, int T, int D, const bf16_t *W, const bf16_t *bias, int N,
@@ -162,15 +194,68 @@ hipError_t launch_rows(const bf16_t *x, int T, int D, const bf16_t *W, const bf1
 // ---------------------------------------------------------------------------------------------
 // K1: router logits + the shared expert's gate logit
 
-template <int MAXT>
+template <int MAXT, bool NORM>
 __global__ __launch_bounds__(256) void decode_router_kernel(DecodeJob j) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = blockIdx.x * 4 + wave;
-    if (r < j.E)
-        router_row<MAXT>(j.x, j.T, j.D, j.router + (size_t)r * j.D,
-                         j.router_bias ? j.router_bias + r : nullptr, j.logits + r, j.E, lane);
-    else if (r == j.E && j.S)
-        router_row<MAXT>(j.x, j.T, j.D, j.sh_gate_w, j.sh_gate_b, j.sh_logit, 1, lane);
+    const int D = j.D;
+    const bf16_t *w = nullptr, *bias = nullptr;
+    bf16_t *out = nullptr;
+    int ldo = 1;
+    if (r < j.E) {
+        w = j.router + (size_t)r * D, out = j.logits + r, ldo = j.E;
+        bias = j.router_bias ? j.router_bias + r : nullptr;
+    } else if (r == j.E && j.S) {
+        w = j.sh_gate_w, bias = j.sh_gate_b, out = j.sh_logit;
+    }
+    // the weight row's first pass is loaded before anything waits (the norm below, in particular)
+    Row4 first{};
+    if (w) first = load_row4(w, lane * 8, D);
+    const bf16_t *x = j.x;
+    if (NORM) {
+        // fused RMSNorm: the workgroup normalises the T rows of norm_src into LDS (wave v takes
+        // rows v, v + 4, ...; row_rms_inv's order and rounding, so the bits of the norm kernel), and
+        // workgroup 0 also writes them to j.x for K2. A row of D <= 2048 is read once.
+        extern __shared__ __align__(16) bf16_t hs[];
+        const uint4 ones = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+        for (int t = wave; t < j.T; t += 4) {
+            const bf16_t *src = j.norm_src + (size_t)t * D;
+            bf16_t *hrow = &hs[(size_t)t * D], *grow = (bf16_t *)j.x + (size_t)t * D;
+            if (D <= 2048) {
+                const Row4 xv = load_row4(src, lane * 8, D);
+                const Row4 nv = j.norm_w ? load_row4(j.norm_w, lane * 8, D) : Row4{{ones, ones, ones, ones}};
+                float ss = 0.f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (lane * 8 + 512 * i < D) {
+                        float f[8];
+                        unpack8(xv.v[i], f);
+                        ss = sumsq8(f, ss);
+                    }
+                const float inv = rms_inv_of(group_sum<64>(ss), D, j.eps);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int d = lane * 8 + 512 * i;
+                    if (d < D) {
+                        const uint4 h = norm8(xv.v[i], inv, nv.v[i]);
+                        *(uint4 *)(hrow + d) = h;
+                        if (blockIdx.x == 0) *(uint4 *)(grow + d) = h;
+                    }
+                }
+            } else {
+                const float inv = row_rms_inv(src, nullptr, D, j.eps, lane);
+                for (int d = lane * 8; d < D; d += 512) {
+                    const uint4 nv = j.norm_w ? *(const uint4 *)(j.norm_w + d) : ones;
+                    const uint4 h = norm8(*(const uint4 *)(src + d), inv, nv);
+                    *(uint4 *)(hrow + d) = h;
+                    if (blockIdx.x == 0) *(uint4 *)(grow + d) = h;
+                }
+            }
+        }
+        __syncthreads();
+        x = hs;
+    }
+    if (w) router_row<MAXT>(x, j.T, D, w, first, bias, out, ldo, lane);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -396,7 +481,9 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeJob j) {
             const float sg = rbf(sigmoidf_(bf2f(shl[t])));
             r = rbf(r + rbf(sg * ysh[t][dd]));
         }
-        j.out[(size_t)t * j.D + d0 + dd] = (bf16_t)f2bf(r);
+        bf16_t *o = j.out + (size_t)t * j.D + d0 + dd;
+        if (j.residual) r = rbf(bf2f(j.residual[(size_t)t * j.D + d0 + dd]) + r);  // R(x + MoE(h))
+        *o = (bf16_t)f2bf(r);
     }
 }
 
@@ -405,7 +492,9 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeJob j) {
 template <int MAXT>
 static void launch_k1(const DecodeJob &j, hipStream_t s) {
     dim3 grid((j.E + (j.S ? 1 : 0) + 3) / 4);
-    decode_router_kernel<MAXT><<<grid, 256, 0, s>>>(j);
+    if (j.norm_src)
+        decode_router_kernel<MAXT, true><<<grid, 256, 2 * (size_t)j.T * j.D, s>>>(j);
+    else decode_router_kernel<MAXT, false><<<grid, 256, 0, s>>>(j);
 }
 
 template <int LPR, int CPL>

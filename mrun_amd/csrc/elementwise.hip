@@ -110,25 +110,10 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const bf16_t *x,
     const int r = blockIdx.x;
     const bf16_t *xr = x + (size_t)r * D;
     const bf16_t *rr = res ? res + (size_t)r * D : nullptr;
-    float ss = 0.f;
-    for (int d = threadIdx.x * 8; d < D; d += 2048) {
-        float xf[8];
-        unpack8(*(const uint4 *)(xr + d), xf);
-        if (rr) {
-            float rf[8];
-            unpack8(*(const uint4 *)(rr + d), rf);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) xf[i] = rbf(xf[i] + rf[i]);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) ss += xf[i] * xf[i];
-    }
-    __shared__ float red[4];
-    ss = group_sum<64>(ss);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    // every wave forms the row's 1/rms itself, in the order the fused decode router uses
+    const float inv = row_rms_inv(xr, rr, D, eps, threadIdx.x & 63);
+    // the row is read in full before any element is written (h may alias x or res)
     __syncthreads();
-    const float tot = ((red[0] + red[1]) + red[2]) + red[3];
-    const float inv = 1.0f / sqrtf(tot / (float)D + eps);
     for (int d = threadIdx.x * 8; d < D; d += 2048) {
         float xf[8];
         unpack8(*(const uint4 *)(xr + d), xf);

@@ -128,6 +128,13 @@ struct DecodeJob {
     bf16_t *sh_act;   // [T, S]
     bf16_t *act;      // [T*k, I], pair p = t*k + j
     bf16_t *out;      // [T, D]
+    // Decoder-layer fusion (the layer stack): with norm_src set, K1 forms the block input
+    // x = R(R(norm_src * rsqrt(mean(norm_src^2) + eps)) * norm_w) itself into LDS (norm_w null:
+    // weight 1; 2*T*D bytes <= 64 KiB) and its workgroup 0 writes it to `x` for K2; with residual
+    // set, K3 writes
+    // out = R(residual + block output) (out may alias residual).
+    const bf16_t *norm_src, *norm_w, *residual;
+    float eps;
 };
 bool decode_supported(int D, int I, int S, int T, int k, int E);
 hipError_t launch_decode(const DecodeJob &job, hipStream_t stream, StageMarks *marks);

@@ -318,8 +318,18 @@ static bool is_decode(const mrun_sparse_moe &m, int T) {
 // ---------------------------------------------------------------------------------------------
 // SparseMoe::forward (moe.rs:149-174)
 
+// The decoder layer around a decode-schedule block (the layer stack): the block's input x is
+// written by its first launch as the RMSNorm of `src` (weight w or ones), and its last launch
+// writes out = R(src + block output).
+struct FusedNorm {
+    const bf16_t *src;
+    const bf16_t *w;
+    float eps;
+};
+
 static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int T, bf16_t *out,
-                                 char *ws, size_t ws_bytes, hipStream_t s, Stages *stg = nullptr) {
+                                 char *ws, size_t ws_bytes, hipStream_t s, Stages *stg = nullptr,
+                                 const FusedNorm *fn = nullptr) {
     Stages none;
     Stages &st = stg ? *stg : none;
     if (st.events && st.n_events > 0) (void)hipEventRecord(st.events[0], s);
@@ -369,9 +379,14 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
         }
         j.logits = logits, j.sh_logit = sh_logit, j.sh_act = sh_act, j.act = act, j.out = out;
         j.ids = ids, j.scores = scores, j.topk_in_kernel = T <= 4;
+        if (fn) {  // K1 normalises fn->src into x; K3 adds the residual
+            if (!m.gate.weight || (S && !m.shared_expert_gate.weight))
+                return Err(MRUN_ERR_UNSUPPORTED, "fused norm needs a dense router and shared gate");
+            j.norm_src = fn->src, j.norm_w = fn->w, j.eps = fn->eps, j.residual = fn->src;
+        }
         // quantized router or shared gate (8-bit in mlx-community conversions): their logits come
         // from the generic products, and the decode launches start at the routed experts
-        if (!m.gate.weight || (S && !m.shared_expert_gate.weight)) {
+        if (!fn && (!m.gate.weight || (S && !m.shared_expert_gate.weight))) {
             TRY(tensor::linear(x, T, m.gate, logits, s));
             if (S) TRY(tensor::linear(x, T, m.shared_expert_gate, sh_logit, s));
             j.router_done = 1;
@@ -729,8 +744,20 @@ int mrun_moe_stack_forward(const mrun_sparse_moe *layers, int32_t n_layers,
         bf16_t *o = (bf16_t *)(ws + blk + a256(2 * (size_t)tokens * D));
         hipStream_t s = (hipStream_t)stream;
         auto wl = [&](int l) { return norm_w ? norm_w[l] : nullptr; };
-        st = hip_status(launch_rms_norm(x, nullptr, wl(0), tokens, D, eps, nullptr, h, s), "stack norm");
-        for (int32_t l = 0; st.ok() && l < n_layers; ++l) {
+        // decode-sized chunks with dense routers: the norm runs inside each block's router launch
+        // and the residual add inside its last launch (three launches per layer, no norm kernel)
+        bool fused = models::is_decode(layers[0], tokens) &&
+                     2 * (size_t)tokens * D <= 65536;  // the normalised rows fit the router's LDS
+        for (int32_t l = 0; fused && l < n_layers; ++l)
+            fused = layers[l].gate.weight && (c.shared_intermediate == 0 ||
+                                              layers[l].shared_expert_gate.weight);
+        for (int32_t l = 0; fused && st.ok() && l < n_layers; ++l) {
+            const models::FusedNorm fn{x, wl(l), eps};
+            st = models::sparse_moe_forward(layers[l], h, tokens, x, ws, blk, s, nullptr, &fn);
+        }
+        if (!fused)
+            st = hip_status(launch_rms_norm(x, nullptr, wl(0), tokens, D, eps, nullptr, h, s), "stack norm");
+        for (int32_t l = 0; !fused && st.ok() && l < n_layers; ++l) {
             st = models::sparse_moe_forward(layers[l], h, tokens, o, ws, blk, s);
             if (!st.ok()) break;
             // x = R(x + o), and the next layer's input h = rms_norm(x) (the last h is unused)
