@@ -8,7 +8,6 @@ typedef uint16_t bf16_t;
 
 namespace mrun {
 
-// bf16 bits <-> f32. Rounding is to nearest even; NaN stays NaN (quiet).
 // Workgroup barrier that waits for this wave's LDS (and scalar) operations only: global loads
 // issued before it stay in flight. __syncthreads also waits for every outstanding vector memory
 // operation (vmcnt(0)), which turns loads issued several steps ahead into loads waited for at the
@@ -18,6 +17,7 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// bf16 bits <-> f32. Rounding is to nearest even; NaN stays NaN (quiet).
 __device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }

@@ -283,6 +283,36 @@ __device__ __forceinline__ void all_topk(const DecodeJob &j, bool compute, uint3
     __syncthreads();
 }
 
+// The slot-th set bit of the expert mask (words mask[0..nw), nw <= 16), i.e. the slot-th active
+// expert in ascending order, or -1 past the last; one wave, all words at once: lane l holds word l
+// and the inclusive count of set bits up to it (a scan over the 16 lanes of DPP row 0), the word
+// is the number of words whose count is <= slot, and the bit within it is found by halving.
+__device__ __forceinline__ int slot_expert(const uint32_t *mask, int nw, int slot, int lane) {
+    const uint32_t mw = mask[lane & 15];
+    const int cnt = lane < nw ? __popc(mw) : 0;
+    int inc = cnt;
+    inc += __builtin_amdgcn_mov_dpp(inc, 0x111, 0xF, 0xF, true);  // row_shr:1 (0 past the row)
+    inc += __builtin_amdgcn_mov_dpp(inc, 0x112, 0xF, 0xF, true);  // row_shr:2
+    inc += __builtin_amdgcn_mov_dpp(inc, 0x114, 0xF, 0xF, true);  // row_shr:4
+    inc += __builtin_amdgcn_mov_dpp(inc, 0x118, 0xF, 0xF, true);  // row_shr:8
+    const int w = __popcll(__ballot(lane < nw && inc <= slot));
+    if (w >= nw) return -1;
+    uint32_t m = mw;
+    int r = slot - (inc - cnt), pos = 0;  // rank of the bit within this lane's word
+#pragma unroll
+    for (int h = 16; h >= 1; h >>= 1) {
+        const int c = __popc(m & ((1u << h) - 1u));
+        const bool up = r >= c;
+        r = up ? r - c : r;
+        m = up ? m >> h : m;
+        pos = up ? pos + h : pos;
+    }
+    const int bit = __builtin_amdgcn_readlane(pos, w);
+    // the bit is set by construction; checked so that an index past the experts cannot come out
+    const uint32_t word = (uint32_t)__builtin_amdgcn_readlane((int)mw, w);
+    return ((word >> bit) & 1u) ? w * 32 + bit : -1;
+}
+
 // Pairs choosing expert e, as a 128-bit set (one wave, from LDS).
 __device__ __forceinline__ void pairs_of(const uint32_t *sid, int P, int e, int lane,
                                          uint64_t &pm0, uint64_t &pm1) {
@@ -341,19 +371,7 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeJob j) {
                 j.scores[threadIdx.x] = ssc[threadIdx.x];
             }
         }
-        // the slot-th active expert, experts in ascending order
-        e = -1;
-        int n = 0;
-        for (int w = 0; w < (j.E + 31) / 32; ++w) {
-            const uint32_t mw = mask[w];
-            const int c = __popc(mw);
-            if (e < 0 && slot < n + c) {
-                uint32_t m = mw;
-                for (int i = 0; i < slot - n; ++i) m &= m - 1;
-                e = w * 32 + __ffs(m) - 1;
-            }
-            n += c;
-        }
+        e = slot_expert(mask, (j.E + 31) / 32, slot, lane);
         if (e < 0) return;
         pairs_of(sid, j.T * j.k, e, lane, pm0, pm1);
         row_base = (rb * 4 + wave) * RG * RPI, a_div = j.k, ldo = j.I, out = j.act;
@@ -422,7 +440,9 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeJob j) {
     load_act(p_lo);
     sid[min((int)threadIdx.x, P - 1)] = my_id;
     ssc[min((int)threadIdx.x, P - 1)] = (bf16_t)my_sc;
-    __syncthreads();
+    // LDS only: the loads above stay in flight, so the routed weight rows (which need sid) are
+    // issued as soon as the routing has arrived, not after the activations and shared rows
+    lds_barrier();
 
     // work: for each pair p (expert sid[p]) its NRG row groups of this workgroup's rows; a wave
     // takes PB pairs at a time and issues all their loads before computing
