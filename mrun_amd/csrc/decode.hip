@@ -517,13 +517,23 @@ static void launch_k1(const DecodeJob &j, hipStream_t s) {
     else decode_router_kernel<MAXT, false><<<grid, 256, 0, s>>>(j);
 }
 
+template <int LPR, int CPL, int PB, int DR>
+static void launch_k3_pb(const DecodeJob &j, hipStream_t s);
+
 template <int LPR, int CPL>
 static void launch_k3_s(const DecodeJob &j, hipStream_t s) {
     // 4 output rows per workgroup; pairs per load batch keep a batch's activations and weight rows
-    // within ~128 registers
+    // within ~128 registers, and are no more than a wave's pairs (a wave takes ceil(P / 4) pairs;
+    // slots past them would load their last pair again)
     constexpr int DR = 4;
     constexpr int NRG = DR / (64 / LPR) > 0 ? DR / (64 / LPR) : 1;
     constexpr int PB = (NRG * CPL <= 2) ? 4 : (NRG * CPL <= 4 ? 2 : 1);
+    if (PB == 4 && (j.T * j.k + 3) / 4 <= 2) launch_k3_pb<LPR, CPL, 2, DR>(j, s);
+    else launch_k3_pb<LPR, CPL, PB, DR>(j, s);
+}
+
+template <int LPR, int CPL, int PB, int DR>
+static void launch_k3_pb(const DecodeJob &j, hipStream_t s) {
     dim3 grid(j.D / DR);
     const int sch = j.S ? j.S >> 5 : 16;
     if (sch == 16) decode_down_kernel<LPR, CPL, 16, 1, PB, DR><<<grid, 256, 0, s>>>(j);
