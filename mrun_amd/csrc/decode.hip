@@ -261,14 +261,15 @@ __global__ __launch_bounds__(256) void decode_router_kernel(DecodeJob j) {
 // ---------------------------------------------------------------------------------------------
 // shared by K2 and K3: the top-k of every token into LDS, and the active-expert mask
 
+template <int NW>
 __device__ __forceinline__ void all_topk(const DecodeJob &j, bool compute, uint32_t *sid,
                                          bf16_t *ssc, uint32_t *mask) {
-    // token t goes to wave (t + blockIdx.x) % 4: the workgroups sharing a CU spread their top-k
+    // token t goes to wave (t + blockIdx.x) % NW: the workgroups sharing a CU spread their top-k
     // over its four SIMDs
-    const int wave = (int)((threadIdx.x >> 6) + 4 - (blockIdx.x & 3)) & 3;
+    const int wave = (int)((threadIdx.x >> 6) + NW - (blockIdx.x & 3)) % NW;
     if (threadIdx.x < 16) mask[threadIdx.x] = 0;
     if (compute) {
-        for (int t = wave; t < j.T; t += 4)
+        for (int t = wave; t < j.T; t += NW)
             topk_token(j.logits + (size_t)t * j.E, j.E, j.k, j.norm != 0, nullptr, sid + t * j.k,
                        ssc + t * j.k);
     } else {
@@ -279,7 +280,7 @@ __device__ __forceinline__ void all_topk(const DecodeJob &j, bool compute, uint3
         }
     }
     __syncthreads();
-    for (int p = threadIdx.x; p < j.T * j.k; p += 256) atomicOr(&mask[sid[p] >> 5], 1u << (sid[p] & 31));
+    for (int p = threadIdx.x; p < j.T * j.k; p += 64 * NW) atomicOr(&mask[sid[p] >> 5], 1u << (sid[p] & 31));
     __syncthreads();
 }
 
@@ -323,19 +324,19 @@ __device__ __forceinline__ void pairs_of(const uint32_t *sid, int P, int e, int 
 // ---------------------------------------------------------------------------------------------
 // K2: shared + routed gate/up
 
-// K2 workgroups: 4 waves x RG rows of one projection pair each, up to 4 tokens for the shared
+// K2 workgroups: NW waves x RG rows of one projection pair each, up to 4 tokens for the shared
 // expert. Few rows per wave keep several waves per SIMD, so their dependent reductions overlap.
-__host__ __device__ inline int shared_gateup_blocks(const DecodeJob &j, int rg) {
-    return j.S ? (j.S / (4 * rg)) * ((j.T + 3) / 4) : 0;
+__host__ __device__ inline int shared_gateup_blocks(const DecodeJob &j, int rows) {
+    return j.S ? (j.S / rows) * ((j.T + 3) / 4) : 0;
 }
 
-template <int LPR, int CPL, int RG>
-__global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeJob j) {
+template <int LPR, int CPL, int RG, int NW>
+__global__ __launch_bounds__(64 * NW) void decode_gateup_kernel(DecodeJob j) {
     __shared__ uint32_t sid[kMaxP], mask[16];
     __shared__ bf16_t ssc[kMaxP];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     constexpr int RPI = 64 / LPR;
-    const int n_sh = shared_gateup_blocks(j, RG * RPI);
+    const int n_sh = shared_gateup_blocks(j, NW * RG * RPI);
     // one gemv_wave call for both kinds of workgroup (its code is large): pick its operands
     const bool sh = (int)blockIdx.x < n_sh;
     auto pick = [&](const QW &a, const QW &b) {  // field by field: no copy of the arguments
@@ -355,15 +356,15 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeJob j) {
     uint64_t pm0, pm1;
     bf16_t *out;
     if (sh) {  // shared expert gate/up: 4 * RG * RPI rows x up to 4 tokens
-        const int n_row_blocks = j.S / (4 * RG * RPI);
+        const int n_row_blocks = j.S / (NW * RG * RPI);
         const int rb = blockIdx.x % n_row_blocks, t0 = (blockIdx.x / n_row_blocks) * 4;
         const int tn = min(4, j.T - t0);
-        row_base = (rb * 4 + wave) * RG * RPI, a_div = 1, ldo = j.S, out = j.sh_act;
+        row_base = (rb * NW + wave) * RG * RPI, a_div = 1, ldo = j.S, out = j.sh_act;
         pm0 = ((1ull << tn) - 1) << t0, pm1 = 0;
     } else {
-        const int r = blockIdx.x - n_sh, row_blocks = j.I / (4 * RG * RPI);
+        const int r = blockIdx.x - n_sh, row_blocks = j.I / (NW * RG * RPI);
         const int slot = r / row_blocks, rb = r % row_blocks;
-        all_topk(j, j.topk_in_kernel != 0, sid, ssc, mask);
+        all_topk<NW>(j, j.topk_in_kernel != 0, sid, ssc, mask);
         if (r == 0 && j.topk_in_kernel) {  // publish the routing for K3
             const int P = j.T * j.k;
             if ((int)threadIdx.x < P) {
@@ -374,7 +375,7 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeJob j) {
         e = slot_expert(mask, (j.E + 31) / 32, slot, lane);
         if (e < 0) return;
         pairs_of(sid, j.T * j.k, e, lane, pm0, pm1);
-        row_base = (rb * 4 + wave) * RG * RPI, a_div = j.k, ldo = j.I, out = j.act;
+        row_base = (rb * NW + wave) * RG * RPI, a_div = j.k, ldo = j.I, out = j.act;
     }
     gemv_wave<LPR, CPL, RG, true>(w0, w1, e, row_base, j.x, j.D, a_div, pm0, pm1, out, ldo, lane);
 }
@@ -520,6 +521,16 @@ static void launch_k1(const DecodeJob &j, hipStream_t s) {
 template <int LPR, int CPL, int PB, int DR>
 static void launch_k3_pb(const DecodeJob &j, hipStream_t s);
 
+// K2 with RG rows per wave and NW waves per workgroup (I and S multiples of NW * RG)
+template <int RG, int NW>
+static void launch_k2(const DecodeJob &j, int n_ch, hipStream_t s) {
+    dim3 g2(shared_gateup_blocks(j, NW * RG) + (j.I / (NW * RG)) * j.max_slots);
+    if (n_ch <= 64) decode_gateup_kernel<64, 1, RG, NW><<<g2, 64 * NW, 0, s>>>(j);
+    else if (n_ch <= 128) decode_gateup_kernel<64, 2, RG, NW><<<g2, 64 * NW, 0, s>>>(j);
+    else if (n_ch <= 192) decode_gateup_kernel<64, 3, RG, NW><<<g2, 64 * NW, 0, s>>>(j);
+    else decode_gateup_kernel<64, 4, RG, NW><<<g2, 64 * NW, 0, s>>>(j);
+}
+
 template <int LPR, int CPL>
 static void launch_k3_s(const DecodeJob &j, hipStream_t s) {
     // 4 output rows per workgroup; pairs per load batch keep a batch's activations and weight rows
@@ -563,25 +574,12 @@ hipError_t launch_decode(const DecodeJob &j, hipStream_t s, StageMarks *marks) {
     if (marks) marks->mark(s);
 
     const int n_ch = j.D >> 5;
-    // rows per wave: about 1024 routed workgroups at T = 1, 2 and 4 (8, 16, 32 expert slots)
+    // rows per wave: about 1024 routed waves-of-rows at T = 1, 2 and 4 (8, 16, 32 expert slots)
     const int rg = j.T == 1 ? 1 : (j.T == 2 ? 2 : 4);
-    dim3 g2(shared_gateup_blocks(j, rg) + (j.I / (4 * rg)) * j.max_slots);
-    if (rg == 1) {
-        if (n_ch <= 64) decode_gateup_kernel<64, 1, 1><<<g2, 256, 0, s>>>(j);
-        else if (n_ch <= 128) decode_gateup_kernel<64, 2, 1><<<g2, 256, 0, s>>>(j);
-        else if (n_ch <= 192) decode_gateup_kernel<64, 3, 1><<<g2, 256, 0, s>>>(j);
-        else decode_gateup_kernel<64, 4, 1><<<g2, 256, 0, s>>>(j);
-    } else if (rg == 2) {
-        if (n_ch <= 64) decode_gateup_kernel<64, 1, 2><<<g2, 256, 0, s>>>(j);
-        else if (n_ch <= 128) decode_gateup_kernel<64, 2, 2><<<g2, 256, 0, s>>>(j);
-        else if (n_ch <= 192) decode_gateup_kernel<64, 3, 2><<<g2, 256, 0, s>>>(j);
-        else decode_gateup_kernel<64, 4, 2><<<g2, 256, 0, s>>>(j);
-    } else {
-        if (n_ch <= 64) decode_gateup_kernel<64, 1, 4><<<g2, 256, 0, s>>>(j);
-        else if (n_ch <= 128) decode_gateup_kernel<64, 2, 4><<<g2, 256, 0, s>>>(j);
-        else if (n_ch <= 192) decode_gateup_kernel<64, 3, 4><<<g2, 256, 0, s>>>(j);
-        else decode_gateup_kernel<64, 4, 4><<<g2, 256, 0, s>>>(j);
-    }
+    // 4 waves per workgroup: 8 and 16 (fewer redundant top-ks per CU) measured slower
+    if (rg == 1) launch_k2<1, 4>(j, n_ch, s);
+    else if (rg == 2) launch_k2<2, 4>(j, n_ch, s);
+    else launch_k2<4, 4>(j, n_ch, s);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (marks) marks->mark(s);

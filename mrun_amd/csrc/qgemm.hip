@@ -221,13 +221,22 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
     }
 
     const int col = n0 + wn * 32 + fr;
-    const float bias = (!GLU && j.bias && col < j.N) ? bf2f(j.bias[col]) : 0.f;
+    // output rows and bias before any store, in one batch of loads: a load inside each element's
+    // bounds check made every store wait for all outstanding memory operations
+    float bias = 0.f;
+    if (!GLU && j.bias) bias = bf2f(j.bias[min(col, j.N - 1)]);
+    int orow[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        orow[i] = row0 + min(wm * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3), mrows - 1);
+    if (j.o_map) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) orow[i] = (int)j.o_map[orow[i]];
+    }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int r = wm * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
         if (r < mrows && col < j.N) {
-            const int pos = row0 + r;
-            const int orow = j.o_map ? (int)j.o_map[pos] : pos;
             float v;
             if (GLU) {
                 const float g = rbf(acc[0][i]), u = rbf(acc[GLU ? 1 : 0][i]);
@@ -236,7 +245,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
                 v = acc[0][i];
                 if (j.bias) v = rbf(v) + bias;
             }
-            j.out[(size_t)orow * j.ldo + col] = (bf16_t)f2bf(v);
+            j.out[(size_t)orow[i] * j.ldo + col] = (bf16_t)f2bf(v);
         }
     }
 }
@@ -572,13 +581,17 @@ __global__ __launch_bounds__(256 * WM, 2 / WM) void qgemm_kernel(GemmJob j) {
     stage_a(ra0, 0);
     load_a(2, ra0);
     lds_barrier();
-    // K step k: compute k, stage k + 1 from `next` (loaded two steps ago), refill `next` with k + 3
-    auto step = [&](int k, bool super_end, ARegs &next) __attribute__((always_inline)) {
+    // K step k: compute k, stage k + 1 from `next` (loaded two steps ago), refill `next` with k + 3.
+    // pf_a / pf_c (constants at each call) turn off the A / code prefetches of the last four steps,
+    // which would load past the end: the epilogue would wait for them, and a wave keeps its slot
+    // until its loads have returned.
+    auto step = [&](int k, bool super_end, ARegs &next, bool pf_a, bool pf_c)
+                    __attribute__((always_inline)) {
         if (active) compute(k);
         if (k + 1 < nks) {
             if (super_end) {  // next super-step: its codes were loaded one super-step ago
                 store_codes((k + 1) / SS);
-                load_codes(min((k + 1) / SS + 1, nss - 1));
+                if (pf_c) load_codes(min((k + 1) / SS + 1, nss - 1));
                 if ((k + 1) % G_KSC == 0) {
                     if (SBUF == 1) lds_barrier();  // every wave is done with the chunk's scales
                     store_scales((k + 1) / G_KSC);
@@ -587,18 +600,47 @@ __global__ __launch_bounds__(256 * WM, 2 / WM) void qgemm_kernel(GemmJob j) {
             }
             stage_a(next, k + 1);
         }
-        load_a(min(k + 3, nks - 1), next);
+        if (pf_a) load_a(min(k + 3, nks - 1), next);
         lds_barrier();
     };
-    for (int ks = 0; ks < nks; ks += 4) {
-        step(ks, SS == 1, ra1);
-        step(ks + 1, SS <= 2, ra0);
-        step(ks + 2, SS == 1, ra1);
-        step(ks + 3, true, ra0);
+    int ks = 0;
+    for (; ks + 4 < nks; ks += 4) {
+        step(ks, SS == 1, ra1, true, true);
+        step(ks + 1, SS <= 2, ra0, true, true);
+        step(ks + 2, SS == 1, ra1, true, true);
+        step(ks + 3, true, ra0, true, true);
     }
+    // the last four steps (nks is a multiple of 8): only step nks - 4 still loads (A of nks - 1);
+    // no chunk of scales starts inside them
+    static_assert(SS <= 2, "the code prefetch of the last steps assumes super-steps of <= 2");
+    step(ks, SS == 1, ra1, true, SS == 1);
+    step(ks + 1, SS <= 2, ra0, false, false);
+    step(ks + 2, SS == 1, ra1, false, false);
+    step(ks + 3, true, ra0, false, false);
     if (!active) return;
 
-    // epilogue: glu -> R(silu(R(gate)) * R(up)); else R(.) (+ bias: R(R(.) + b))
+    // epilogue: glu -> R(silu(R(gate)) * R(up)); else R(.) (+ bias: R(R(.) + b)). The output rows
+    // of all 32 elements come first, in one batch of index loads (none without o_map): a load
+    // inside each element's bounds check made every store wait for all outstanding memory
+    // operations, the K loop's last prefetches included.
+    int orow[2][16];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            orow[mi][i] = g.row0 + min(wm * 64 + mi * 32 + 8 * (i >> 2) + 4 * fh + (i & 3),
+                                       g.mrows - 1);
+    if (g.o_map) {
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) orow[mi][i] = (int)g.o_map[orow[mi][i]];
+    }
+    float bias_v[2] = {0.f, 0.f};  // R(.) + bias of the two column fragments (no glu)
+    if (!GLU && j.bias) {
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) bias_v[ni] = bf2f(j.bias[min(n0 + wn * 64 + ni * 32 + fr, j.N - 1)]);
+    }
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi) {
         if (GLU) {
@@ -607,26 +649,22 @@ __global__ __launch_bounds__(256 * WM, 2 / WM) void qgemm_kernel(GemmJob j) {
             for (int i = 0; i < 16; ++i) {
                 const int r = wm * 64 + mi * 32 + 8 * (i >> 2) + 4 * fh + (i & 3);
                 if (r < g.mrows && col < j.N) {
-                    const int pos = g.row0 + r;
-                    const int orow = g.o_map ? (int)g.o_map[pos] : pos;
                     const float gt = rbf(acc[mi][0][i]), u = rbf(acc[mi][1][i]);
-                    g.out[(size_t)orow * g.ldo + col] = (bf16_t)f2bf((gt * sigmoidf_(gt)) * u);
+                    g.out[(size_t)orow[mi][i] * g.ldo + col] =
+                        (bf16_t)f2bf((gt * sigmoidf_(gt)) * u);
                 }
             }
         } else {
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni) {
                 const int col = n0 + wn * 64 + ni * 32 + fr;
-                const float bias = (j.bias && col < j.N) ? bf2f(j.bias[col]) : 0.f;
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const int r = wm * 64 + mi * 32 + 8 * (i >> 2) + 4 * fh + (i & 3);
                     if (r < g.mrows && col < j.N) {
-                        const int pos = g.row0 + r;
-                        const int orow = g.o_map ? (int)g.o_map[pos] : pos;
                         float v = acc[mi][ni][i];
-                        if (j.bias) v = rbf(v) + bias;
-                        g.out[(size_t)orow * g.ldo + col] = (bf16_t)f2bf(v);
+                        if (j.bias) v = rbf(v) + bias_v[ni];
+                        g.out[(size_t)orow[mi][i] * g.ldo + col] = (bf16_t)f2bf(v);
                     }
                 }
             }
