@@ -4,8 +4,8 @@
 // column block).
 //
 // Workgroup tile 64 rows x 64 columns, 4 waves of 32 x 32 (v_mfma_f32_32x32x16_bf16), K steps of
-// 64. The loop is latency-bound (a K step is 4 MFMAs per wave), so each thread keeps three K steps
-// of loads in flight in registers (a ring unrolled by three) and the LDS tiles are double-buffered:
+// 64. The loop is latency-bound (a K step is 4 MFMAs per wave), so each thread keeps NST K steps
+// of loads in flight in registers (a ring unrolled by NST) and the LDS tiles are double-buffered:
 // one barrier per K step, which waits for LDS only, so the loads stay in flight across it.
 #include "common.hpp"
 #include "kernels.hpp"
@@ -23,6 +23,7 @@ struct Stage {
     uint4 a0, a1, b0, b1;
 };
 
+template <int NST>
 __global__ __launch_bounds__(256) void dense_gemm_kernel(DenseJob j) {
     __shared__ __align__(16) bf16_t As[2][DBM * DLDK];
     __shared__ __align__(16) bf16_t Bs[2][DBN * DLDK];
@@ -72,25 +73,27 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(DenseJob j) {
                 __builtin_bit_cast(bf16x8_t, *(const uint4 *)(a + 16 * s)),
                 __builtin_bit_cast(bf16x8_t, *(const uint4 *)(b + 16 * s)), acc, 0, 0, 0);
     };
-    // step ks: its loads (issued three steps earlier) go to LDS buffer ks & 1, the registers are
-    // refilled with step ks + 3, then the tile is multiplied
+    // step ks: its loads (issued NST steps earlier) go to LDS buffer ks & 1, the registers are
+    // refilled with step ks + NST, then the tile is multiplied
     auto step = [&](int ks, Stage st) __attribute__((always_inline)) -> Stage {
         store(ks, st);
         lds_barrier();
-        const Stage nx = load(min(ks + 3, nks - 1));  // clamped: the tail reloads a valid step
+        const Stage nx = load(min(ks + NST, nks - 1));  // clamped: the tail reloads a valid step
         compute(ks);
         return nx;
     };
 
-    Stage s0 = load(0), s1 = load(min(1, nks - 1)), s2 = load(min(2, nks - 1));
+    Stage ring[NST];
+#pragma unroll
+    for (int i = 0; i < NST; ++i) ring[i] = load(min(i, nks - 1));
     int ks = 0;
-    for (; ks + 3 <= nks; ks += 3) {
-        s0 = step(ks, s0);
-        s1 = step(ks + 1, s1);
-        s2 = step(ks + 2, s2);
+    for (; ks + NST <= nks; ks += NST) {
+#pragma unroll
+        for (int i = 0; i < NST; ++i) ring[i] = step(ks + i, ring[i]);
     }
-    if (ks < nks) s0 = step(ks, s0);
-    if (ks + 1 < nks) s1 = step(ks + 1, s1);
+#pragma unroll
+    for (int i = 0; i < NST - 1; ++i)
+        if (ks + i < nks) ring[i] = step(ks + i, ring[i]);
 
     const int col = n0 + wn * 32 + fr;
     const float bv = (bias && col < N) ? bf2f(bias[col]) : 0.f;
@@ -114,7 +117,8 @@ hipError_t launch_dense_gemm(const DenseJob &j, hipStream_t stream) {
         return hipErrorInvalidValue;
     const int nb = (j.N0 + DBN - 1) / DBN + (j.W1 ? (j.N1 + DBN - 1) / DBN : 0);
     dim3 grid((j.M + DBM - 1) / DBM, nb);
-    dense_gemm_kernel<<<grid, 256, 0, stream>>>(j);
+    // a deeper ring (4, 6, 8 steps) measured no faster: the steps are not bound by load latency
+    dense_gemm_kernel<3><<<grid, 256, 0, stream>>>(j);
     return hipGetLastError();
 }
 
