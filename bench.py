@@ -4,11 +4,12 @@ Default workload: one Qwen3.6-35B-A3B-like block (hidden 2
 top-8 with norm_topk_prob, expert FFN 512, shared expert 512), 4-bit affine group-64 weights,
 synthetic seeded data, decode T = 1. A step is one block forward over the batch. The JSON line
 also carries the T = 2, 4, 16 decode sweep, the configs[2] prefill (T = 2048, Zipf-skewed
-router) and the configs[3] stack of 40 layers (T = 1 and T = 4096) measured the same way, the dominant kernel's roofline (HIP events on the launch stream)
-and the CPU restatement timed on a bounded sample on this host.
+router), the configs[3] stack of 40 layers (T = 1 and T = 4096) and the configs[4] Coder-shaped
+block (T = 1, 8, 8192) measured the same way, the dominant kernel's roofline (HIP events on the
+launch stream) and the CPU restatement timed on a bounded sample on this host.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens T] [--no-cpu] [--no-prefill]
-                    [--no-stack] [--stack-only] [--prefill-only]
+                    [--no-stack] [--no-coder] [--stack-only] [--prefill-only] [--coder-only]
 """
 from __future__ import annotations
 
@@ -271,6 +272,38 @@ def stack_point(args, Q, M, synth, torch) -> dict:
     return out
 
 
+def coder_point(args, M, synth, torch) -> dict:
+    """the Coder-shaped block (hidden 6144, 160 experts, top-8, FFN 2560, no shared
+    expert; 4.2 GB of 4-bit weights, generated on the device) at decode T = 1 and 8, where a block
+    streams 8 experts' 26.5 MB each, and at prefill T = 8192."""
+    C = synth.CODER
+    print("[bench] coder configs[4]: generating the block on the device", file=sys.stderr,
+          flush=True)
+    dev = M.device_block(C, synth.CFG_CODER, 0)
+    torch.cuda.synchronize()
+    out = {"workload": "configs[4]: Coder-shaped block (hidden 6144, 160 experts, top-8, "
+                       "FFN 2560, no shared expert), 4-bit affine group 64"}
+    for T, steps in ((1, max(args.steps // 4, 20)), (8, max(args.steps // 4, 20)), (8192, 3)):
+        print(f"[bench] coder T={T}", file=sys.stderr, flush=True)
+        x = M.bf16_tensor(synth.make_x(C, T, config=synth.CFG_CODER, layer=T))
+        wall, dev_ms, _ = time_forward(dev, x, steps, 2 if T > 16 else 10, torch)
+        pt = {"tokens": T, "steps": steps, "ms_per_step": wall, "device_ms": dev_ms,
+              "tokens_per_s": T / (wall * 1e-3)}
+        if T <= 16:
+            _, _, ids, _ = dev.router_forward(x)
+            n_active = int(np.unique(M.u32_array(ids)).size)
+            b = decode_bytes(C, n_active, T)["block"]
+            pt.update(n_active=n_active, bytes=b, hbm_frac=b / (dev_ms * 1e-3) / HBM_PEAK)
+        else:
+            f = prefill_flops(C, T)["block"]
+            pt.update(flops=f, mfma_frac=f / (dev_ms * 1e-3) / MFMA_BF16_PEAK)
+        out[f"T{T}"] = pt
+        del x
+    del dev
+    torch.cuda.empty_cache()
+    return out
+
+
 def measured_traffic(kernel: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 byte counters, or None."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
@@ -295,6 +328,9 @@ def main(argv=None) -> int:
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-stack", action="store_true")
     ap.add_argument("--stack-layers", type=int, default=40)
+    ap.add_argument("--no-coder", action="store_true")
+    ap.add_argument("--coder-only", action="store_true",
+                    help="only the configs[4] Coder-shaped block; prints its own JSON line")
     ap.add_argument("--stack-only", action="store_true",
                     help="only the configs[3] layer stack; prints its own JSON line")
     ap.add_argument("--prefill-only", action="store_true",
@@ -327,6 +363,9 @@ def main(argv=None) -> int:
         return 0
     if args.stack_only:
         print(json.dumps({"stack": stack_point(args, Q, M, synth, torch)}), flush=True)
+        return 0
+    if args.coder_only:
+        print(json.dumps({"coder": coder_point(args, M, synth, torch)}), flush=True)
         return 0
     print(f"[bench] generating the configs[1] block ({Q.name})", file=sys.stderr, flush=True)
     hb = synth.make_block(Q, config=synth.CFG_DECODE)
@@ -372,6 +411,7 @@ def main(argv=None) -> int:
 
     prefill = None if args.no_prefill else prefill_point(args, Q, M, synth, torch)
     stack = None if args.no_stack else stack_point(args, Q, M, synth, torch)
+    coder = None if args.no_coder else coder_point(args, M, synth, torch)
 
     cpu = None
     if not args.no_cpu:
@@ -405,6 +445,7 @@ def main(argv=None) -> int:
         "sweep": sweep,
         "prefill": prefill,
         "stack": stack,
+        "coder": coder,
     }
     print(json.dumps(line), flush=True)
     return 0

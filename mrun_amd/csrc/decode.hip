@@ -325,18 +325,21 @@ __device__ __forceinline__ void pairs_of(const uint32_t *sid, int P, int e, int 
 // K2: shared + routed gate/up
 
 // K2 workgroups: NW waves x RG rows of one projection pair each, up to 4 tokens for the shared
-// expert. Few rows per wave keep several waves per SIMD, so their dependent reductions overlap.
+// expert, for gu_loop consecutive row blocks in turn (a routed workgroup derives the routing once
+// for all of them). Few rows per wave keep several waves per SIMD, so their dependent reductions
+// overlap; the loop keeps the workgroup count near one resident round for wide experts.
 __host__ __device__ inline int shared_gateup_blocks(const DecodeJob &j, int rows) {
     return j.S ? (j.S / rows) * ((j.T + 3) / 4) : 0;
 }
 
-template <int LPR, int CPL, int RG, int NW>
+template <int LPR, int CPL, int RG, int NW, bool LOOP>
 __global__ __launch_bounds__(64 * NW) void decode_gateup_kernel(DecodeJob j) {
     __shared__ uint32_t sid[kMaxP], mask[16];
     __shared__ bf16_t ssc[kMaxP];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     constexpr int RPI = 64 / LPR;
-    const int n_sh = shared_gateup_blocks(j, NW * RG * RPI);
+    const int L = LOOP ? j.gu_loop : 1;
+    const int n_sh = shared_gateup_blocks(j, NW * RG * RPI * L);
     // one gemv_wave call for both kinds of workgroup (its code is large): pick its operands
     const bool sh = (int)blockIdx.x < n_sh;
     auto pick = [&](const QW &a, const QW &b) {  // field by field: no copy of the arguments
@@ -352,18 +355,20 @@ __global__ __launch_bounds__(64 * NW) void decode_gateup_kernel(DecodeJob j) {
         return q;
     };
     const QW w0 = pick(j.sg, j.wg), w1 = pick(j.su, j.wu);
-    int e = 0, row_base, a_div, ldo;
+    int e = 0, rb, a_div, ldo;
     uint64_t pm0, pm1;
     bf16_t *out;
     if (sh) {  // shared expert gate/up: 4 * RG * RPI rows x up to 4 tokens
-        const int n_row_blocks = j.S / (NW * RG * RPI);
-        const int rb = blockIdx.x % n_row_blocks, t0 = (blockIdx.x / n_row_blocks) * 4;
+        const int n_row_blocks = j.S / (NW * RG * RPI * L);
+        rb = blockIdx.x % n_row_blocks;
+        const int t0 = (blockIdx.x / n_row_blocks) * 4;
         const int tn = min(4, j.T - t0);
-        row_base = (rb * NW + wave) * RG * RPI, a_div = 1, ldo = j.S, out = j.sh_act;
+        a_div = 1, ldo = j.S, out = j.sh_act;
         pm0 = ((1ull << tn) - 1) << t0, pm1 = 0;
     } else {
-        const int r = blockIdx.x - n_sh, row_blocks = j.I / (NW * RG * RPI);
-        const int slot = r / row_blocks, rb = r % row_blocks;
+        const int r = blockIdx.x - n_sh, row_blocks = j.I / (NW * RG * RPI * L);
+        const int slot = r / row_blocks;
+        rb = r % row_blocks;
         all_topk<NW>(j, j.topk_in_kernel != 0, sid, ssc, mask);
         if (r == 0 && j.topk_in_kernel) {  // publish the routing for K3
             const int P = j.T * j.k;
@@ -375,9 +380,16 @@ __global__ __launch_bounds__(64 * NW) void decode_gateup_kernel(DecodeJob j) {
         e = slot_expert(mask, (j.E + 31) / 32, slot, lane);
         if (e < 0) return;
         pairs_of(sid, j.T * j.k, e, lane, pm0, pm1);
-        row_base = (rb * NW + wave) * RG * RPI, a_div = j.k, ldo = j.I, out = j.act;
+        a_div = j.k, ldo = j.I, out = j.act;
     }
-    gemv_wave<LPR, CPL, RG, true>(w0, w1, e, row_base, j.x, j.D, a_div, pm0, pm1, out, ldo, lane);
+    if (LOOP) {
+        for (int l = 0; l < L; ++l)
+            gemv_wave<LPR, CPL, RG, true>(w0, w1, e, ((rb * L + l) * NW + wave) * RG * RPI, j.x,
+                                          j.D, a_div, pm0, pm1, out, ldo, lane);
+    } else {
+        gemv_wave<LPR, CPL, RG, true>(w0, w1, e, (rb * NW + wave) * RG * RPI, j.x, j.D, a_div, pm0,
+                                      pm1, out, ldo, lane);
+    }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -521,14 +533,31 @@ static void launch_k1(const DecodeJob &j, hipStream_t s) {
 template <int LPR, int CPL, int PB, int DR>
 static void launch_k3_pb(const DecodeJob &j, hipStream_t s);
 
-// K2 with RG rows per wave and NW waves per workgroup (I and S multiples of NW * RG)
+// K2 with RG rows per wave and NW waves per workgroup (I and S multiples of NW * RG). At T = 1
+// with rows wider than 2048, each workgroup runs gu_loop row blocks, the smallest power of two
+// that keeps the routed workgroups at 1024 or fewer (I and S multiples of NW * RG * gu_loop): a
+// workgroup per row block there would derive the routing 8 times as often and run in several
+// rounds (Coder shape: 71 -> 63 us). Narrower rows (one round already) and T > 1 (measured
+// slower with the loop) take one row block per workgroup.
+template <int RG, int NW, bool LOOP>
+static void launch_k2_l(const DecodeJob &j, int n_ch, dim3 g2, hipStream_t s) {
+    if (n_ch <= 64) decode_gateup_kernel<64, 1, RG, NW, LOOP><<<g2, 64 * NW, 0, s>>>(j);
+    else if (n_ch <= 128) decode_gateup_kernel<64, 2, RG, NW, LOOP><<<g2, 64 * NW, 0, s>>>(j);
+    else if (n_ch <= 192) decode_gateup_kernel<64, 3, RG, NW, LOOP><<<g2, 64 * NW, 0, s>>>(j);
+    else decode_gateup_kernel<64, 4, RG, NW, LOOP><<<g2, 64 * NW, 0, s>>>(j);
+}
+
 template <int RG, int NW>
-static void launch_k2(const DecodeJob &j, int n_ch, hipStream_t s) {
-    dim3 g2(shared_gateup_blocks(j, NW * RG) + (j.I / (NW * RG)) * j.max_slots);
-    if (n_ch <= 64) decode_gateup_kernel<64, 1, RG, NW><<<g2, 64 * NW, 0, s>>>(j);
-    else if (n_ch <= 128) decode_gateup_kernel<64, 2, RG, NW><<<g2, 64 * NW, 0, s>>>(j);
-    else if (n_ch <= 192) decode_gateup_kernel<64, 3, RG, NW><<<g2, 64 * NW, 0, s>>>(j);
-    else decode_gateup_kernel<64, 4, RG, NW><<<g2, 64 * NW, 0, s>>>(j);
+static void launch_k2(DecodeJob j, int n_ch, hipStream_t s) {
+    const int per_slot = j.I / (NW * RG), sh_blocks = j.S / (NW * RG);
+    int L = 1;
+    while (RG == 1 && j.T == 1 && n_ch > 64 && j.max_slots * per_slot / L > 1024 &&
+           per_slot % (2 * L) == 0 && sh_blocks % (2 * L) == 0)
+        L *= 2;
+    j.gu_loop = L;
+    dim3 g2(shared_gateup_blocks(j, NW * RG * L) + (j.I / (NW * RG * L)) * j.max_slots);
+    if (RG == 1 && L > 1) launch_k2_l<1, NW, true>(j, n_ch, g2, s);
+    else launch_k2_l<RG, NW, false>(j, n_ch, g2, s);
 }
 
 template <int LPR, int CPL>
