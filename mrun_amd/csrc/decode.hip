@@ -87,6 +87,44 @@ __device__ __forceinline__ void gemv_wave(const QW &w0, const QW &w1, int e, int
     }
 }
 
+// One token (T = 1), rows row0 + l * row_step (l < L) of w0 and w1 with GLU: the activation row
+// is loaded and re-paired once, and the next rows' weights are loaded before the current rows are
+// computed (the last iteration is peeled, so no load sits under a condition). One row per wave
+// (LPR = 64).
+template <int CPL>
+__device__ __forceinline__ void gemv_wave_stream(const QW &w0, const QW &w1, int e, int row0,
+                                                 int row_step, int L, const bf16_t *arow,
+                                                 bf16_t *orow, int lane) {
+    const int n_ch = w0.in >> 5;
+    XRaw xr[CPL];
+    load_xrow_raw<CPL>(arow, lane, 64, n_ch, xr);
+    WRow<CPL> c0, c1, n0, n1;
+    load_wrow<CPL>(w0, e, row0, lane, 64, c0);
+    load_wrow<CPL>(w1, e, row0, lane, 64, c1);
+    XChunk xc[CPL];
+    pair_xrow<CPL>(xr, xc);
+    auto emit = [&](const WRow<CPL> &g, const WRow<CPL> &u, int row) __attribute__((always_inline)) {
+        const float a0 = group_sum<64>(row_part(g, xc)), a1 = group_sum<64>(row_part(u, xc));
+        if (lane == 0 && row < w0.out) {
+            const float gt = rbf(a0), up = rbf(a1);
+            orow[row] = (bf16_t)f2bf((gt * sigmoidf_(gt)) * up);
+        }
+    };
+    int row = row0;
+    for (int l = 0; l + 1 < L; ++l, row += row_step) {
+        load_wrow<CPL>(w0, e, row + row_step, lane, 64, n0);
+        load_wrow<CPL>(w1, e, row + row_step, lane, 64, n1);
+        opaque_row(c0);
+        opaque_row(c1);
+        emit(c0, c1, row);
+        c0 = n0;
+        c1 = n1;
+    }
+    opaque_row(c0);
+    opaque_row(c1);
+    emit(c0, c1, row);
+}
+
 // Eight bf16 of a raw row through the RMSNorm: R(R(x * inv) * w), w eight bf16 (or ones).
 __device__ __forceinline__ uint4 norm8(uint4 x, float inv, uint4 w) {
     const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, ws[4] = {w.x, w.y, w.z, w.w};
@@ -382,10 +420,12 @@ __global__ __launch_bounds__(64 * NW) void decode_gateup_kernel(DecodeJob j) {
         pairs_of(sid, j.T * j.k, e, lane, pm0, pm1);
         a_div = j.k, ldo = j.I, out = j.act;
     }
-    if (LOOP) {
-        for (int l = 0; l < L; ++l)
-            gemv_wave<LPR, CPL, RG, true>(w0, w1, e, ((rb * L + l) * NW + wave) * RG * RPI, j.x,
-                                          j.D, a_div, pm0, pm1, out, ldo, lane);
+    if (LOOP) {  // T = 1, RG = 1, LPR = 64: the one pair's rows rb * L * NW + wave + NW * l
+        static_assert(!LOOP || (RG == 1 && LPR == 64), "the streaming loop takes one row per wave");
+        if (pm0 == 0) return;
+        const int p = __ffsll((unsigned long long)pm0) - 1;
+        gemv_wave_stream<CPL>(w0, w1, e, rb * L * NW + wave, NW, L,
+                              j.x + (size_t)(p / a_div) * j.D, out + (size_t)p * ldo, lane);
     } else {
         gemv_wave<LPR, CPL, RG, true>(w0, w1, e, (rb * NW + wave) * RG * RPI, j.x, j.D, a_div, pm0,
                                       pm1, out, ldo, lane);
