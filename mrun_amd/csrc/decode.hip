@@ -560,6 +560,70 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeJob j) {
     }
 }
 
+// K3 for one token without a shared expert and down rows of more than 2048 inputs: wave w takes
+// pair w (its expert's down rows for the workgroup's drs output rows), loads and pairs the
+// activation row once and streams the rows in batches of RB, the next batch loaded before the
+// current one is computed; then the combine of the workgroup's rows from LDS. Each row's dot and
+// every rounding are those of decode_down_kernel with LPR = 64 (the same bits).
+constexpr int kStreamMaxRows = 64;
+
+template <int CPL, int RB>
+__global__ __launch_bounds__(512) void decode_down_stream_kernel(DecodeJob j, int drs) {
+    __shared__ float yv[8][kStreamMaxRows];
+    __shared__ bf16_t ssc[8];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int P = j.k;  // T = 1: pair p = expert choice p
+    const int d0 = blockIdx.x * drs;
+    if (wave < P) {
+        const int e = (int)j.ids[wave];
+        XRaw xr[CPL];
+        load_xrow_raw<CPL>(j.act + (size_t)wave * j.I, lane, 64, j.I >> 5, xr);
+        WRow<CPL> cur[RB], nxt[RB];
+#pragma unroll
+        for (int b = 0; b < RB; ++b) load_wrow<CPL>(j.wd, e, d0 + b, lane, 64, cur[b]);
+        const uint32_t sc = j.scores[wave];
+        XChunk xc[CPL];
+        pair_xrow<CPL>(xr, xc);
+        auto emit = [&](int r) __attribute__((always_inline)) {
+#pragma unroll
+            for (int b = 0; b < RB; ++b) opaque_row(cur[b]);
+#pragma unroll
+            for (int b = 0; b < RB; ++b) {
+                const float y = group_sum<64>(row_part(cur[b], xc));
+                if (lane == 0) yv[wave][r + b] = rbf(y);
+            }
+        };
+        int r = 0;
+        for (; r + RB < drs; r += RB) {
+#pragma unroll
+            for (int b = 0; b < RB; ++b) load_wrow<CPL>(j.wd, e, d0 + r + RB + b, lane, 64, nxt[b]);
+            emit(r);
+#pragma unroll
+            for (int b = 0; b < RB; ++b) cur[b] = nxt[b];
+        }
+        emit(r);
+        if (lane == 0) ssc[wave] = (bf16_t)sc;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < drs; i += blockDim.x) {
+        float acc = 0.f;
+        for (int jj = 0; jj < P; ++jj) acc += rbf(yv[jj][i] * bf2f(ssc[jj]));
+        float r = rbf(acc);
+        if (j.residual) r = rbf(bf2f(j.residual[d0 + i]) + r);  // R(x + MoE(h))
+        j.out[d0 + i] = (bf16_t)f2bf(r);
+    }
+}
+
+// whether the streaming K3 takes the job: rows per workgroup D / 256 (every CU one workgroup), a
+// multiple of the batch of 4 rows
+static int stream_k3_rows(const DecodeJob &j) {
+    const int ich = j.I >> 5;
+    // (at most 3 chunks of 32 per lane: 4 would spill)
+    if (j.T != 1 || j.S != 0 || j.k > 8 || ich <= 64 || ich > 192 || j.D % 256 != 0) return 0;
+    const int drs = j.D / 256;
+    return (drs % 4 == 0 && drs <= kStreamMaxRows) ? drs : 0;
+}
+
 // ---------------------------------------------------------------------------------------------
 
 template <int MAXT>
@@ -654,7 +718,11 @@ hipError_t launch_decode(const DecodeJob &j, hipStream_t s, StageMarks *marks) {
     if (marks) marks->mark(s);
 
     const int ich = j.I >> 5;
-    if (ich == 16) launch_k3_s<16, 1>(j, s);
+    if (const int drs = stream_k3_rows(j)) {
+        const dim3 g3(j.D / drs), b3(64 * j.k);
+        if (ich <= 128) decode_down_stream_kernel<2, 4><<<g3, b3, 0, s>>>(j, drs);
+        else decode_down_stream_kernel<3, 4><<<g3, b3, 0, s>>>(j, drs);
+    } else if (ich == 16) launch_k3_s<16, 1>(j, s);
     else if (ich < 64) launch_k3_s<32, 2>(j, s);
     else if (ich <= 64) launch_k3_s<64, 1>(j, s);
     else if (ich <= 128) launch_k3_s<64, 2>(j, s);
