@@ -282,6 +282,24 @@ def test_block_coder_prefill_rows():
     run_block(hb, dev, x_np, f"Coder prefill T={T} (32 sampled rows)", check_rows=np.sort(rows))
 
 
+def test_coder_stack_matches_layer_loop():
+    """Two Coder-shaped layers (configs[4] weights, the second layer's seeds) in the layer stack at
+    T = 1: the streaming decode kernels with the fused norm and residual add give the bits of the
+    loop of single ops (rms_norm, block forward, add_rms_norm)."""
+    layers = [_coder_dev(), M.device_block(synth.CODER, synth.CFG_CODER, 1)]
+    st = M.MoeStack(layers, None, 1e-6)
+    x_np = synth.make_x(synth.CODER, 1, config=synth.CFG_CODER, layer=77)
+    got = M.bf16_bits(st.forward_(M.bf16_tensor(x_np)))
+    x = M.bf16_tensor(x_np)
+    h = M.rms_norm(x, None, 1e-6)
+    for layer in layers:
+        o = layer.forward(h)
+        x, h = M.add_rms_norm(x, o, None, 1e-6)
+    torch.cuda.synchronize()
+    assert np.array_equal(got, M.bf16_bits(x)), "Coder stack differs from the op loop"
+    assert np.isfinite(synth.bf16_to_f32(got)).all()
+
+
 _CODER = {}
 
 
