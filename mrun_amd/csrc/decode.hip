@@ -92,9 +92,9 @@ __device__ __forceinline__ void gemv_wave(const QW &w0, const QW &w1, int e, int
 // computed (the last iteration is peeled, so no load sits under a condition). One row per wave
 // (LPR = 64).
 template <int CPL>
-__device__ __forceinline__ void gemv_wave_stream(const QW &w0, const QW &w1, int e, int row0,
-                                                 int row_step, int L, const bf16_t *arow,
-                                                 bf16_t *orow, int lane) {
+__device__ __forceinline__ void gemv_wave_stream1(const QW &w0, const QW &w1, int e, int row0,
+                                                  int row_step, int L, const bf16_t *arow,
+                                                  bf16_t *orow, int lane) {
     const int n_ch = w0.in >> 5;
     XRaw xr[CPL];
     load_xrow_raw<CPL>(arow, lane, 64, n_ch, xr);
@@ -123,6 +123,71 @@ __device__ __forceinline__ void gemv_wave_stream(const QW &w0, const QW &w1, int
     opaque_row(c0);
     opaque_row(c1);
     emit(c0, c1, row);
+}
+
+// Rows row0 + l * row_step (l < L) of w0 and w1 with GLU for the pairs in pm0 | pm1, NP pairs at
+// a time: their activation rows are loaded and re-paired once, and the next rows' weights are
+// loaded before the current rows are computed (the last iteration is peeled, so no load sits under
+// a condition). Pair p reads A row p / a_div and writes output row p. One row per wave (LPR = 64).
+template <int CPL, int NP>
+__device__ __forceinline__ void gemv_wave_stream(const QW &w0, const QW &w1, int e, int row0,
+                                                 int row_step, int L, const bf16_t *A, int lda,
+                                                 int a_div, uint64_t pm0, uint64_t pm1,
+                                                 bf16_t *out, int ldo, int lane) {
+    const int n_ch = w0.in >> 5;
+    auto next = [&]() -> int {
+        if (pm0) {
+            const int p = __ffsll((unsigned long long)pm0) - 1;
+            pm0 &= pm0 - 1;
+            return p;
+        }
+        if (pm1) {
+            const int p = 64 + __ffsll((unsigned long long)pm1) - 1;
+            pm1 &= pm1 - 1;
+            return p;
+        }
+        return -1;
+    };
+    for (int p0 = next(); p0 >= 0; p0 = next()) {
+        int pp[NP];
+        pp[0] = p0;
+#pragma unroll
+        for (int q = 1; q < NP; ++q) pp[q] = next();  // -1: no pair in this slot
+        XRaw xr[NP][CPL];
+#pragma unroll
+        for (int q = 0; q < NP; ++q)
+            load_xrow_raw<CPL>(A + (size_t)(max(pp[q], p0) / a_div) * lda, lane, 64, n_ch, xr[q]);
+        WRow<CPL> c0, c1, n0, n1;
+        load_wrow<CPL>(w0, e, row0, lane, 64, c0);
+        load_wrow<CPL>(w1, e, row0, lane, 64, c1);
+        XChunk xc[NP][CPL];
+#pragma unroll
+        for (int q = 0; q < NP; ++q) pair_xrow<CPL>(xr[q], xc[q]);
+        auto emit = [&](int row) __attribute__((always_inline)) {
+            opaque_row(c0);
+            opaque_row(c1);
+#pragma unroll
+            for (int q = 0; q < NP; ++q) {
+                if (pp[q] >= 0) {
+                    const float a0 = group_sum<64>(row_part(c0, xc[q]));
+                    const float a1 = group_sum<64>(row_part(c1, xc[q]));
+                    if (lane == 0 && row < w0.out) {
+                        const float gt = rbf(a0), up = rbf(a1);
+                        out[(size_t)pp[q] * ldo + row] = (bf16_t)f2bf((gt * sigmoidf_(gt)) * up);
+                    }
+                }
+            }
+        };
+        int row = row0;
+        for (int l = 0; l + 1 < L; ++l, row += row_step) {
+            load_wrow<CPL>(w0, e, row + row_step, lane, 64, n0);
+            load_wrow<CPL>(w1, e, row + row_step, lane, 64, n1);
+            emit(row);
+            c0 = n0;
+            c1 = n1;
+        }
+        emit(row);
+    }
 }
 
 // Eight bf16 of a raw row through the RMSNorm: R(R(x * inv) * w), w eight bf16 (or ones).
@@ -370,7 +435,7 @@ __host__ __device__ inline int shared_gateup_blocks(const DecodeJob &j, int rows
     return j.S ? (j.S / rows) * ((j.T + 3) / 4) : 0;
 }
 
-template <int LPR, int CPL, int RG, int NW, bool LOOP>
+template <int LPR, int CPL, int RG, int NW, int LOOP>
 __global__ __launch_bounds__(64 * NW) void decode_gateup_kernel(DecodeJob j) {
     __shared__ uint32_t sid[kMaxP], mask[16];
     __shared__ bf16_t ssc[kMaxP];
@@ -420,12 +485,17 @@ __global__ __launch_bounds__(64 * NW) void decode_gateup_kernel(DecodeJob j) {
         pairs_of(sid, j.T * j.k, e, lane, pm0, pm1);
         a_div = j.k, ldo = j.I, out = j.act;
     }
-    if (LOOP) {  // T = 1, RG = 1, LPR = 64: the one pair's rows rb * L * NW + wave + NW * l
+    if (LOOP) {  // RG = 1, LPR = 64: rows rb * L * NW + wave + NW * l, LOOP pairs at a time
         static_assert(!LOOP || (RG == 1 && LPR == 64), "the streaming loop takes one row per wave");
-        if (pm0 == 0) return;
-        const int p = __ffsll((unsigned long long)pm0) - 1;
-        gemv_wave_stream<CPL>(w0, w1, e, rb * L * NW + wave, NW, L,
-                              j.x + (size_t)(p / a_div) * j.D, out + (size_t)p * ldo, lane);
+        if (LOOP == 1) {  // one token: one pair
+            if (pm0 == 0) return;
+            const int p = __ffsll((unsigned long long)pm0) - 1;
+            gemv_wave_stream1<CPL>(w0, w1, e, rb * L * NW + wave, NW, L,
+                                   j.x + (size_t)(p / a_div) * j.D, out + (size_t)p * ldo, lane);
+        } else {
+            gemv_wave_stream<CPL, LOOP ? LOOP : 1>(w0, w1, e, rb * L * NW + wave, NW, L, j.x, j.D,
+                                                   a_div, pm0, pm1, out, ldo, lane);
+        }
     } else {
         gemv_wave<LPR, CPL, RG, true>(w0, w1, e, (rb * NW + wave) * RG * RPI, j.x, j.D, a_div, pm0,
                                       pm1, out, ldo, lane);
@@ -638,13 +708,13 @@ static void launch_k1(const DecodeJob &j, hipStream_t s) {
 template <int LPR, int CPL, int PB, int DR>
 static void launch_k3_pb(const DecodeJob &j, hipStream_t s);
 
-// K2 with RG rows per wave and NW waves per workgroup (I and S multiples of NW * RG). At T = 1
-// with rows wider than 2048, each workgroup runs gu_loop row blocks, the smallest power of two
-// that keeps the routed workgroups at 1024 or fewer (I and S multiples of NW * RG * gu_loop): a
-// workgroup per row block there would derive the routing 8 times as often and run in several
-// rounds (Coder shape: 71 -> 63 us). Narrower rows (one round already) and T > 1 (measured
-// slower with the loop) take one row block per workgroup.
-template <int RG, int NW, bool LOOP>
+// K2 with RG rows per wave and NW waves per workgroup (I and S multiples of NW * RG). With rows
+// wider than 2048 (one row per wave), each workgroup streams gu_loop row blocks, the smallest
+// power of two that keeps the routed workgroups at 1024 or fewer (I and S multiples of
+// NW * RG * gu_loop): a workgroup per row block derived the routing once per block, ran in several
+// rounds and had one block's loads in flight at a time. Narrower rows (one round already) take
+// one row block per workgroup (the loop measured slower there).
+template <int RG, int NW, int LOOP>
 static void launch_k2_l(const DecodeJob &j, int n_ch, dim3 g2, hipStream_t s) {
     if (n_ch <= 64) decode_gateup_kernel<64, 1, RG, NW, LOOP><<<g2, 64 * NW, 0, s>>>(j);
     else if (n_ch <= 128) decode_gateup_kernel<64, 2, RG, NW, LOOP><<<g2, 64 * NW, 0, s>>>(j);
@@ -656,13 +726,15 @@ template <int RG, int NW>
 static void launch_k2(DecodeJob j, int n_ch, hipStream_t s) {
     const int per_slot = j.I / (NW * RG), sh_blocks = j.S / (NW * RG);
     int L = 1;
-    while (RG == 1 && j.T == 1 && n_ch > 64 && j.max_slots * per_slot / L > 1024 &&
+    while (RG == 1 && n_ch > 64 && j.max_slots * per_slot / L > 1024 &&
            per_slot % (2 * L) == 0 && sh_blocks % (2 * L) == 0)
         L *= 2;
     j.gu_loop = L;
     dim3 g2(shared_gateup_blocks(j, NW * RG * L) + (j.I / (NW * RG * L)) * j.max_slots);
-    if (RG == 1 && L > 1) launch_k2_l<1, NW, true>(j, n_ch, g2, s);
-    else launch_k2_l<RG, NW, false>(j, n_ch, g2, s);
+    // one token: one pair per expert; more: the activation rows of 2 pairs held at a time
+    if (RG == 1 && L > 1 && j.T == 1) launch_k2_l<1, NW, 1>(j, n_ch, g2, s);
+    else if (RG == 1 && L > 1) launch_k2_l<1, NW, 2>(j, n_ch, g2, s);  // pair by pair: slower
+    else launch_k2_l<RG, NW, 0>(j, n_ch, g2, s);
 }
 
 template <int LPR, int CPL>
@@ -709,7 +781,8 @@ hipError_t launch_decode(const DecodeJob &j, hipStream_t s, StageMarks *marks) {
 
     const int n_ch = j.D >> 5;
     // rows per wave: about 1024 routed waves-of-rows at T = 1, 2 and 4 (8, 16, 32 expert slots)
-    const int rg = j.T == 1 ? 1 : (j.T == 2 ? 2 : 4);
+    // rows wider than 2048 take one row per wave and the streaming loop at every T
+    const int rg = (j.T == 1 || n_ch > 64) ? 1 : (j.T == 2 ? 2 : 4);
     // 4 waves per workgroup: 8 and 16 (fewer redundant top-ks per CU) measured slower
     if (rg == 1) launch_k2<1, 4>(j, n_ch, s);
     else if (rg == 2) launch_k2<2, 4>(j, n_ch, s);
