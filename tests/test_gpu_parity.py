@@ -282,6 +282,28 @@ def test_block_coder_prefill_rows():
     run_block(hb, dev, x_np, f"Coder prefill T={T} (32 sampled rows)", check_rows=np.sort(rows))
 
 
+WIDE_SHARED = synth.Shape(hidden=4096, experts=64, top_k=8, intermediate=1024, shared=1024)
+
+
+@pytest.mark.parametrize("T", [1, 2, 5])
+def test_wide_rows_with_shared_expert(T):
+    """Rows wider than 2048 with a shared expert: the decode gate/up streams two row blocks per
+    workgroup (routed and shared workgroups; one pair at T = 1, two pairs at a time above), the
+    down kernel is the general one. Against the oracle on the GPU's expert choices."""
+    if "wide" not in _CODER:
+        hb = synth.make_block(WIDE_SHARED, config=synth.CFG_DECODE, layer=7)
+        _CODER["wide"] = (hb, M.SparseMoe(hb))
+    hb, dev = _CODER["wide"]
+    x_np = synth.make_x(WIDE_SHARED, T, config=synth.CFG_DECODE, layer=300 + T)
+    run_block(hb, dev, x_np, f"wide rows + shared expert T={T}")
+    # row-exactness: every row equals its one-row forward
+    if T > 1:
+        batch = M.bf16_bits(dev.forward(M.bf16_tensor(x_np)))
+        for t in range(T):
+            one = M.bf16_bits(dev.forward(M.bf16_tensor(x_np[t:t + 1])))
+            assert np.array_equal(one[0], batch[t]), f"row {t}"
+
+
 def test_coder_stack_matches_layer_loop():
     """Two Coder-shaped layers (configs[4] weights, the second layer's seeds) in the layer stack at
     T = 1: the streaming decode kernels with the fused norm and residual add give the bits of the
