@@ -92,18 +92,6 @@ __device__ __forceinline__ float wave_max(float v) {
 
 __device__ __forceinline__ uint32_t umax_(uint32_t a, uint32_t b) { return a > b ? a : b; }
 
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    v = umax_(v, dpp_u32<0xB1>(v));
-    v = umax_(v, dpp_u32<0x4E>(v));
-    v = umax_(v, dpp_u32<0x141>(v));
-    v = umax_(v, dpp_u32<0x140>(v));
-    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
-    const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
-    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
-    const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
-    return umax_(umax_(r0, r1), umax_(r2, r3));
-}
-
 // Eight bf16 (one uint4) dotted with eight f32 codes.
 __device__ __forceinline__ void unpack8(const uint4 &v, float *f) {
     f[0] = bf_lo(v.x); f[1] = bf_hi(v.x);

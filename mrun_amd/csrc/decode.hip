@@ -10,8 +10,11 @@
 //                expert's gate/up rows for its pairs. The first routed workgroup publishes the
 //                routing for K3.
 //   K3 down    : prefetches the shared expert's down rows, reads the routing, computes the routed
-//                down rows of every active expert for its 8 output rows, then the combine:
+//                down rows of every active expert for its 4 output rows, then the combine:
 //                out = R(R(sum_j R(y[t,j] * s[t,j])) + R(R(sigmoid(g_t)) * shared[t])).
+// Rows wider than 2048 (the Coder shape): a K2 workgroup streams several row blocks with the next
+// rows loaded before the current ones are computed, and at T = 1 without a shared expert K3 takes
+// one wave per pair streaming that expert's down rows. Every row keeps the same bits.
 // Pair p = t*k + j indexes the activations (act [T*k, I]), so no argsort is needed at decode; the
 // results are the same as the sorted dispatch's, row by row.
 #include "common.hpp"
