@@ -12,9 +12,9 @@
 //   K3 down    : prefetches the shared expert's down rows, reads the routing, computes the routed
 //                down rows of every active expert for its 4 output rows, then the combine:
 //                out = R(R(sum_j R(y[t,j] * s[t,j])) + R(R(sigmoid(g_t)) * shared[t])).
-// Rows wider than 2048 (the Coder shape): a K2 workgroup streams several row blocks with the next
-// rows loaded before the current ones are computed, and at T = 1 without a shared expert K3 takes
-// one wave per pair streaming that expert's down rows. Every row keeps the same bits.
+// Rows wider than 2048 (the Coder shape): a K2 workgroup streams several row blocks pair by pair
+// with the next rows loaded before the current ones are computed, and without a shared expert K3
+// takes one wave per pair streaming that expert's down rows. Every row keeps the same bits.
 // Pair p = t*k + j indexes the activations (act [T*k, I]), so no argsort is needed at decode; the
 // results are the same as the sorted dispatch's, row by row.
 #include "common.hpp"
@@ -90,10 +90,9 @@ __device__ __forceinline__ void gemv_wave(const QW &w0, const QW &w1, int e, int
     }
 }
 
-// One token (T = 1), rows row0 + l * row_step (l < L) of w0 and w1 with GLU: the activation row
-// is loaded and re-paired once, and the next rows' weights are loaded before the current rows are
-// computed (the last iteration is peeled, so no load sits under a condition). One row per wave
-// (LPR = 64).
+// One pair, rows row0 + l * row_step (l < L) of w0 and w1 with GLU: the activation row is loaded
+// and re-paired once, and the next rows' weights are loaded before the current rows are computed
+// (the last iteration is peeled, so no load sits under a condition). One row per wave (LPR = 64).
 template <int CPL>
 __device__ __forceinline__ void gemv_wave_stream1(const QW &w0, const QW &w1, int e, int row0,
                                                   int row_step, int L, const bf16_t *arow,
@@ -126,71 +125,6 @@ __device__ __forceinline__ void gemv_wave_stream1(const QW &w0, const QW &w1, in
     opaque_row(c0);
     opaque_row(c1);
     emit(c0, c1, row);
-}
-
-// Rows row0 + l * row_step (l < L) of w0 and w1 with GLU for the pairs in pm0 | pm1, NP pairs at
-// a time: their activation rows are loaded and re-paired once, and the next rows' weights are
-// loaded before the current rows are computed (the last iteration is peeled, so no load sits under
-// a condition). Pair p reads A row p / a_div and writes output row p. One row per wave (LPR = 64).
-template <int CPL, int NP>
-__device__ __forceinline__ void gemv_wave_stream(const QW &w0, const QW &w1, int e, int row0,
-                                                 int row_step, int L, const bf16_t *A, int lda,
-                                                 int a_div, uint64_t pm0, uint64_t pm1,
-                                                 bf16_t *out, int ldo, int lane) {
-    const int n_ch = w0.in >> 5;
-    auto next = [&]() -> int {
-        if (pm0) {
-            const int p = __ffsll((unsigned long long)pm0) - 1;
-            pm0 &= pm0 - 1;
-            return p;
-        }
-        if (pm1) {
-            const int p = 64 + __ffsll((unsigned long long)pm1) - 1;
-            pm1 &= pm1 - 1;
-            return p;
-        }
-        return -1;
-    };
-    for (int p0 = next(); p0 >= 0; p0 = next()) {
-        int pp[NP];
-        pp[0] = p0;
-#pragma unroll
-        for (int q = 1; q < NP; ++q) pp[q] = next();  // -1: no pair in this slot
-        XRaw xr[NP][CPL];
-#pragma unroll
-        for (int q = 0; q < NP; ++q)
-            load_xrow_raw<CPL>(A + (size_t)(max(pp[q], p0) / a_div) * lda, lane, 64, n_ch, xr[q]);
-        WRow<CPL> c0, c1, n0, n1;
-        load_wrow<CPL>(w0, e, row0, lane, 64, c0);
-        load_wrow<CPL>(w1, e, row0, lane, 64, c1);
-        XChunk xc[NP][CPL];
-#pragma unroll
-        for (int q = 0; q < NP; ++q) pair_xrow<CPL>(xr[q], xc[q]);
-        auto emit = [&](int row) __attribute__((always_inline)) {
-            opaque_row(c0);
-            opaque_row(c1);
-#pragma unroll
-            for (int q = 0; q < NP; ++q) {
-                if (pp[q] >= 0) {
-                    const float a0 = group_sum<64>(row_part(c0, xc[q]));
-                    const float a1 = group_sum<64>(row_part(c1, xc[q]));
-                    if (lane == 0 && row < w0.out) {
-                        const float gt = rbf(a0), up = rbf(a1);
-                        out[(size_t)pp[q] * ldo + row] = (bf16_t)f2bf((gt * sigmoidf_(gt)) * up);
-                    }
-                }
-            }
-        };
-        int row = row0;
-        for (int l = 0; l + 1 < L; ++l, row += row_step) {
-            load_wrow<CPL>(w0, e, row + row_step, lane, 64, n0);
-            load_wrow<CPL>(w1, e, row + row_step, lane, 64, n1);
-            emit(row);
-            c0 = n0;
-            c1 = n1;
-        }
-        emit(row);
-    }
 }
 
 // Eight bf16 of a raw row through the RMSNorm: R(R(x * inv) * w), w eight bf16 (or ones).
@@ -438,8 +372,12 @@ __host__ __device__ inline int shared_gateup_blocks(const DecodeJob &j, int rows
     return j.S ? (j.S / rows) * ((j.T + 3) / 4) : 0;
 }
 
-template <int LPR, int CPL, int RG, int NW, int LOOP>
-__global__ __launch_bounds__(64 * NW) void decode_gateup_kernel(DecodeJob j) {
+// (the streaming kernel with 3 chunks per lane is held to 168 registers, 3 waves per SIMD: at 171
+// it ran 2, and T = 1 took 4 us longer on the Coder shape)
+template <int LPR, int CPL, int RG, int NW, bool LOOP>
+__global__ __launch_bounds__(64 * NW)
+__attribute__((amdgpu_waves_per_eu(LOOP && CPL == 3 ? 3 : 1))) void decode_gateup_kernel(
+    DecodeJob j) {
     __shared__ uint32_t sid[kMaxP], mask[16];
     __shared__ bf16_t ssc[kMaxP];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -488,16 +426,19 @@ __global__ __launch_bounds__(64 * NW) void decode_gateup_kernel(DecodeJob j) {
         pairs_of(sid, j.T * j.k, e, lane, pm0, pm1);
         a_div = j.k, ldo = j.I, out = j.act;
     }
-    if (LOOP) {  // RG = 1, LPR = 64: rows rb * L * NW + wave + NW * l, LOOP pairs at a time
+    if (LOOP) {  // RG = 1, LPR = 64: rows rb * L * NW + wave + NW * l, pair by pair
         static_assert(!LOOP || (RG == 1 && LPR == 64), "the streaming loop takes one row per wave");
-        if (LOOP == 1) {  // one token: one pair
-            if (pm0 == 0) return;
-            const int p = __ffsll((unsigned long long)pm0) - 1;
-            gemv_wave_stream1<CPL>(w0, w1, e, rb * L * NW + wave, NW, L,
-                                   j.x + (size_t)(p / a_div) * j.D, out + (size_t)p * ldo, lane);
-        } else {
-            gemv_wave_stream<CPL, LOOP ? LOOP : 1>(w0, w1, e, rb * L * NW + wave, NW, L, j.x, j.D,
-                                                   a_div, pm0, pm1, out, ldo, lane);
+        // (two pairs' activations held at a time measured slower: 256 registers, one wave per SIMD)
+        for (;;) {
+            int p;
+            if (pm0) p = __ffsll((unsigned long long)pm0) - 1, pm0 &= pm0 - 1;
+            else if (pm1) p = 64 + __ffsll((unsigned long long)pm1) - 1, pm1 &= pm1 - 1;
+            else break;
+            // opaque, so nothing of one pair's pass (row addresses) is held over for the next
+            int row0 = rb * L * NW + wave;
+            asm volatile("" : "+v"(row0));
+            gemv_wave_stream1<CPL>(w0, w1, e, row0, NW, L, j.x + (size_t)(p / a_div) * j.D,
+                                   out + (size_t)p * ldo, lane);
         }
     } else {
         gemv_wave<LPR, CPL, RG, true>(w0, w1, e, (rb * NW + wave) * RG * RPI, j.x, j.D, a_div, pm0,
@@ -633,28 +574,29 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeJob j) {
     }
 }
 
-// K3 for one token without a shared expert and down rows of more than 2048 inputs: wave w takes
-// pair w (its expert's down rows for the workgroup's drs output rows), loads and pairs the
-// activation row once and streams the rows in batches of RB, the next batch loaded before the
-// current one is computed; then the combine of the workgroup's rows from LDS. Each row's dot and
-// every rounding are those of decode_down_kernel with LPR = 64 (the same bits).
-constexpr int kStreamMaxRows = 64, kStreamBatch = 2;
+// K3 without a shared expert and down rows of more than 2048 inputs: wave w takes pairs w, w + 8,
+// ... (each pair's expert's down rows for the workgroup's drs output rows): it loads and pairs the
+// pair's activation row once and streams the rows in batches of RB, the next batch loaded before
+// the current one is computed; then the combine of the workgroup's rows for every token from
+// LDS. Each row's dot and every rounding are those of decode_down_kernel with LPR = 64 (the same
+// bits).
+constexpr int kStreamMaxRows = 32, kStreamBatch = 2;
 
 template <int CPL, int RB>
 __global__ __launch_bounds__(512) void decode_down_stream_kernel(DecodeJob j, int drs) {
-    __shared__ float yv[8][kStreamMaxRows];
-    __shared__ bf16_t ssc[8];
+    __shared__ float yv[kMaxP][kStreamMaxRows];
+    __shared__ bf16_t ssc[kMaxP];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int P = j.k;  // T = 1: pair p = expert choice p
+    const int P = j.T * j.k;
     const int d0 = blockIdx.x * drs;
-    if (wave < P) {
-        const int e = (int)j.ids[wave];
+    for (int p = wave; p < P; p += 8) {
+        const int e = (int)j.ids[p];
         XRaw xr[CPL];
-        load_xrow_raw<CPL>(j.act + (size_t)wave * j.I, lane, 64, j.I >> 5, xr);
+        load_xrow_raw<CPL>(j.act + (size_t)p * j.I, lane, 64, j.I >> 5, xr);
         WRow<CPL> cur[RB], nxt[RB];
 #pragma unroll
         for (int b = 0; b < RB; ++b) load_wrow<CPL>(j.wd, e, d0 + b, lane, 64, cur[b]);
-        const uint32_t sc = j.scores[wave];
+        const uint32_t sc = j.scores[p];
         XChunk xc[CPL];
         pair_xrow<CPL>(xr, xc);
         auto emit = [&](int r) __attribute__((always_inline)) {
@@ -663,7 +605,7 @@ __global__ __launch_bounds__(512) void decode_down_stream_kernel(DecodeJob j, in
 #pragma unroll
             for (int b = 0; b < RB; ++b) {
                 const float y = group_sum<64>(row_part(cur[b], xc));
-                if (lane == 0) yv[wave][r + b] = rbf(y);
+                if (lane == 0) yv[p][r + b] = rbf(y);
             }
         };
         int r = 0;
@@ -675,15 +617,20 @@ __global__ __launch_bounds__(512) void decode_down_stream_kernel(DecodeJob j, in
             for (int b = 0; b < RB; ++b) cur[b] = nxt[b];
         }
         emit(r);
-        if (lane == 0) ssc[wave] = (bf16_t)sc;
+        if (lane == 0) ssc[p] = (bf16_t)sc;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < drs; i += blockDim.x) {
+    for (int i = threadIdx.x; i < j.T * drs; i += blockDim.x) {
+        const int t = i / drs, dd = i % drs;
         float acc = 0.f;
-        for (int jj = 0; jj < P; ++jj) acc += rbf(yv[jj][i] * bf2f(ssc[jj]));
+        for (int jj = 0; jj < j.k; ++jj) {
+            const int p = t * j.k + jj;
+            acc += rbf(yv[p][dd] * bf2f(ssc[p]));
+        }
         float r = rbf(acc);
-        if (j.residual) r = rbf(bf2f(j.residual[d0 + i]) + r);  // R(x + MoE(h))
-        j.out[d0 + i] = (bf16_t)f2bf(r);
+        const size_t o = (size_t)t * j.D + d0 + dd;
+        if (j.residual) r = rbf(bf2f(j.residual[o]) + r);  // R(x + MoE(h))
+        j.out[o] = (bf16_t)f2bf(r);
     }
 }
 
@@ -693,7 +640,7 @@ __global__ __launch_bounds__(512) void decode_down_stream_kernel(DecodeJob j, in
 static int stream_k3_rows(const DecodeJob &j) {
     const int ich = j.I >> 5;
     // (at most 3 chunks of 32 per lane: 4 would spill)
-    if (j.T != 1 || j.S != 0 || j.k > 8 || ich <= 64 || ich > 192 || j.D % 512 != 0) return 0;
+    if (j.S != 0 || ich <= 64 || ich > 192 || j.D % 512 != 0) return 0;
     const int drs = j.D / 512;
     return (drs % kStreamBatch == 0 && drs <= kStreamMaxRows) ? drs : 0;
 }
@@ -713,11 +660,12 @@ static void launch_k3_pb(const DecodeJob &j, hipStream_t s);
 
 // K2 with RG rows per wave and NW waves per workgroup (I and S multiples of NW * RG). With rows
 // wider than 2048 (one row per wave), each workgroup streams gu_loop row blocks, the smallest
-// power of two that keeps the routed workgroups at 1024 or fewer (I and S multiples of
+// power of two that keeps the routed workgroups at 1024 per token or fewer (I and S multiples of
 // NW * RG * gu_loop): a workgroup per row block derived the routing once per block, ran in several
-// rounds and had one block's loads in flight at a time. Narrower rows (one round already) take
-// one row block per workgroup (the loop measured slower there).
-template <int RG, int NW, int LOOP>
+// rounds and had one block's loads in flight at a time. (On the 6144 x 2560 Coder shape this is 8
+// row blocks at T = 1 to 16; caps of 512, 2048 and 4096 per token measured slower.) Narrower rows
+// (one round already) take one row block per workgroup (the loop measured slower there).
+template <int RG, int NW, bool LOOP>
 static void launch_k2_l(const DecodeJob &j, int n_ch, dim3 g2, hipStream_t s) {
     if (n_ch <= 64) decode_gateup_kernel<64, 1, RG, NW, LOOP><<<g2, 64 * NW, 0, s>>>(j);
     else if (n_ch <= 128) decode_gateup_kernel<64, 2, RG, NW, LOOP><<<g2, 64 * NW, 0, s>>>(j);
@@ -729,15 +677,13 @@ template <int RG, int NW>
 static void launch_k2(DecodeJob j, int n_ch, hipStream_t s) {
     const int per_slot = j.I / (NW * RG), sh_blocks = j.S / (NW * RG);
     int L = 1;
-    while (RG == 1 && n_ch > 64 && j.max_slots * per_slot / L > 1024 &&
+    while (RG == 1 && n_ch > 64 && j.max_slots * per_slot / L > 1024 * j.T &&
            per_slot % (2 * L) == 0 && sh_blocks % (2 * L) == 0)
         L *= 2;
     j.gu_loop = L;
     dim3 g2(shared_gateup_blocks(j, NW * RG * L) + (j.I / (NW * RG * L)) * j.max_slots);
-    // one token: one pair per expert; more: the activation rows of 2 pairs held at a time
-    if (RG == 1 && L > 1 && j.T == 1) launch_k2_l<1, NW, 1>(j, n_ch, g2, s);
-    else if (RG == 1 && L > 1) launch_k2_l<1, NW, 2>(j, n_ch, g2, s);  // pair by pair: slower
-    else launch_k2_l<RG, NW, 0>(j, n_ch, g2, s);
+    if (RG == 1 && L > 1) launch_k2_l<1, NW, true>(j, n_ch, g2, s);
+    else launch_k2_l<RG, NW, false>(j, n_ch, g2, s);
 }
 
 template <int LPR, int CPL>
@@ -796,7 +742,7 @@ hipError_t launch_decode(const DecodeJob &j, hipStream_t s, StageMarks *marks) {
 
     const int ich = j.I >> 5;
     if (const int drs = stream_k3_rows(j)) {
-        const dim3 g3(j.D / drs), b3(64 * j.k);
+        const dim3 g3(j.D / drs), b3(512);
         if (ich <= 128) decode_down_stream_kernel<2, kStreamBatch><<<g3, b3, 0, s>>>(j, drs);
         else decode_down_stream_kernel<3, kStreamBatch><<<g3, b3, 0, s>>>(j, drs);
     } else if (ich == 16) launch_k3_s<16, 1>(j, s);
