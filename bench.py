@@ -6,7 +6,8 @@ synthetic seeded data, decode T = 1. A step is one block forward over the batch.
 also carries the T = 2, 4, 16 decode sweep, the configs[2] prefill (T = 2048, Zipf-skewed
 router), the configs[3] stack of 40 layers (T = 1 and T = 4096) and the configs[4] Coder-shaped
 block (T = 1, 8, 8192) measured the same way, the dominant kernel's roofline (HIP events on the
-launch stream) and the CPU restatement timed on a bounded sample on this host.
+launch stream), this box's measured copy and MFMA rates beside the published peaks, and the CPU
+restatement timed on a bounded sample on this host (all cores, and one thread).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens T] [--no-cpu] [--no-prefill]
                     [--no-stack] [--no-coder] [--stack-only] [--prefill-only] [--coder-only]
@@ -163,24 +164,99 @@ def time_graph(dev, x, steps: int, torch):
     return ev.ms(0, 1) / steps, out
 
 
-def cpu_baseline(hb, x_np, seconds: float):
-    """The CPU restatement on this host's cores, repeated for about `seconds`."""
+def cpu_baseline(hb, x_np, seconds: float, seconds_1t: float = 4.0):
+    """The CPU restatement on this host's cores, repeated for about `seconds` after one warm-up
+    forward (the median forward is reported), then on one thread for about `seconds_1t`."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import oracle as O
     cores = len(os.sched_getaffinity(0))
-    threads = O.set_threads(cores)
-    O.moe_forward(hb, x_np)  # warm
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        O.moe_forward(hb, x_np)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or reps >= 2000:
-            break
-    per = el / reps
-    return {"value": x_np.shape[0] / per, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{reps} block forwards at T={x_np.shape[0]} ({el:.1f} s), same seeded "
-                      f"block, OpenMP over {threads} threads; us/block {per * 1e6:.0f}"}
+
+    def run(threads, budget):
+        used = O.set_threads(threads)
+        O.moe_forward(hb, x_np)  # warm
+        times, t0 = [], time.perf_counter()
+        while True:
+            t = time.perf_counter()
+            O.moe_forward(hb, x_np)
+            times.append(time.perf_counter() - t)
+            if (time.perf_counter() - t0 >= budget and len(times) >= 5) or len(times) >= 2000:
+                break
+        return used, float(np.median(times)), len(times), time.perf_counter() - t0
+
+    threads, med, reps, el = run(cores, seconds)
+    _, med1, reps1, el1 = run(1, seconds_1t)
+    O.set_threads(cores)
+    T = x_np.shape[0]
+    return {"value": T / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{reps} block forwards at T={T} ({el:.1f} s), same seeded block, OpenMP "
+                      f"over {threads} threads (sched_getaffinity {cores}, hardware "
+                      f"{os.cpu_count()}); median us/block {med * 1e6:.0f}",
+            "one_thread": {"value": T / med1, "unit": "tokens/s", "cores": 1,
+                           "sample": f"{reps1} block forwards ({el1:.1f} s); median us/block "
+                                     f"{med1 * 1e6:.0f}"}}
+
+
+def machine_point(torch) -> dict:
+    """This box's roofline denominators beside the published peaks: a 4 GiB read (larger than the
+    256 MB last-level cache), a 1 GiB device copy (bytes read + written per second) and
+    back-to-back v_mfma_f32_32x32x16_bf16 on every SIMD (flop/s), all with kernels of
+    libmrun_calib.so timed by HIP events on the launch stream."""
+    root = os.path.dirname(os.path.abspath(__file__))
+    lib = ctypes.CDLL(os.path.join(root, "mrun_amd", "lib", "libmrun_calib.so"))
+    lib.mrun_calib_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                    ctypes.c_void_p]
+    lib.mrun_calib_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.mrun_calib_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                    ctypes.c_void_p]
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    ev = Events(2)
+    rbytes = 4 << 30
+    rsrc = torch.ones(rbytes // 4, dtype=torch.int32, device="cuda")
+    rout = torch.empty(lib.mrun_calib_read_threads(), dtype=torch.int32, device="cuda")
+    for _ in range(2):
+        assert lib.mrun_calib_read(rsrc.data_ptr(), rbytes, rout.data_ptr(), sp) == 0
+    rreps = 10
+    ev.record(0, stream)
+    for _ in range(rreps):
+        assert lib.mrun_calib_read(rsrc.data_ptr(), rbytes, rout.data_ptr(), sp) == 0
+    ev.record(1, stream)
+    read_ms = ev.ms(0, 1) / rreps
+    read_bps = rbytes / (read_ms * 1e-3)
+    del rsrc, rout
+    nbytes = 1 << 30
+    src = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        assert lib.mrun_calib_copy(src.data_ptr(), dst.data_ptr(), nbytes, sp) == 0
+    reps = 20
+    ev.record(0, stream)
+    for _ in range(reps):
+        assert lib.mrun_calib_copy(src.data_ptr(), dst.data_ptr(), nbytes, sp) == 0
+    ev.record(1, stream)
+    copy_ms = ev.ms(0, 1) / reps
+    assert bool(torch.equal(src, dst)), "calibration copy differs"
+    copy_bps = 2 * nbytes / (copy_ms * 1e-3)
+    del src, dst
+    blocks, iters = 256 * 12, 4096  # 12 workgroups of 4 waves per CU: 12 waves per SIMD queued
+    chains = lib.mrun_calib_mfma_chains()
+    out = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
+    assert lib.mrun_calib_mfma(blocks, 64, out.data_ptr(), sp) == 0
+    ev.record(0, stream)
+    assert lib.mrun_calib_mfma(blocks, iters, out.data_ptr(), sp) == 0
+    ev.record(1, stream)
+    mfma_ms = ev.ms(0, 1)
+    assert bool((out == float(chains * 256 * iters)).all()), "calibration MFMA sums differ"
+    flops = blocks * 4 * iters * chains * 32 * 32 * 16 * 2
+    mfma_fps = flops / (mfma_ms * 1e-3)
+    return {"read_GBps": read_bps / 1e9, "read_frac_of_peak": read_bps / HBM_PEAK,
+            "read": f"4 GiB, 16-byte loads, mean of {rreps}; {read_ms * 1e3:.0f} us per read",
+            "copy_GBps": copy_bps / 1e9, "copy_frac_of_peak": copy_bps / HBM_PEAK,
+            "copy": f"1 GiB device to device, 16-byte loads/stores, mean of {reps}; "
+                    f"{copy_ms * 1e3:.0f} us per copy",
+            "mfma_bf16_TFLOPs": mfma_fps / 1e12, "mfma_frac_of_peak": mfma_fps / MFMA_BF16_PEAK,
+            "mfma": f"v_mfma_f32_32x32x16_bf16, {blocks} workgroups x 4 waves x {iters} x "
+                    f"{chains} chains; {mfma_ms:.2f} ms"}
 
 
 def prefill_point(args, Q, M, synth, torch) -> dict:
@@ -413,6 +489,9 @@ def main(argv=None) -> int:
     stack = None if args.no_stack else stack_point(args, Q, M, synth, torch)
     coder = None if args.no_coder else coder_point(args, M, synth, torch)
 
+    print("[bench] copy and MFMA calibration", file=sys.stderr, flush=True)
+    machine = machine_point(torch)
+
     cpu = None
     if not args.no_cpu:
         print("[bench] CPU restatement baseline", file=sys.stderr, flush=True)
@@ -442,6 +521,7 @@ def main(argv=None) -> int:
         "stages_us": main_pt["stages_us"],
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "machine": machine,
         "sweep": sweep,
         "prefill": prefill,
         "stack": stack,

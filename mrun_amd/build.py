@@ -3,6 +3,7 @@
 - mrun_amd/lib/libmrun_moe.so   : the HIP kernels for gfx950 + the C ABI (include/mrun_moe.h)
 - mrun_amd/lib/libmrun_synth.so : the seeded input generator (include/mrun_synth.h), host C
 - mrun_amd/lib/libmrun_synth_dev.so : its device variant (HIP)
+- mrun_amd/lib/libmrun_calib.so : copy and MFMA calibration kernels (HIP), loaded by bench.py only
 - oracle/_build/liborc_moe.so   : the CPU restatement used by tests and the CPU baseline
 
 Every HIP translation unit is compiled with packed-FP32 instructions disabled
@@ -94,6 +95,16 @@ def build_synth_dev() -> Path:
     return target
 
 
+def build_calib() -> Path:
+    """Copy and MFMA-rate kernels that measure this box's roofline denominators (bench.py)."""
+    LIB.mkdir(parents=True, exist_ok=True)
+    target = LIB / "libmrun_calib.so"
+    tmp = LIB / "libmrun_calib.so.tmp"
+    _run([HIPCC, *HIP_FLAGS, "-shared", str(CSRC / "calib.hip"), "-o", str(tmp)])
+    os.replace(tmp, target)
+    return target
+
+
 def build_oracle() -> Path:
     """The CPU restatement (test infrastructure); built beside the product, never linked into it."""
     _run(["make", "-s", "-C", str(ROOT / "oracle")])
@@ -103,7 +114,7 @@ def build_oracle() -> Path:
 def build_all() -> list[Path]:
     if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
         raise RuntimeError(f"hipcc not found at {HIPCC}")
-    return [build_synth(), build_synth_dev(), build_oracle(), build_moe()]
+    return [build_synth(), build_synth_dev(), build_calib(), build_oracle(), build_moe()]
 
 
 if __name__ == "__main__":

@@ -34,6 +34,28 @@ def test_every_declared_symbol_is_exported():
     assert b"gfx950" in lib.mrun_version()
 
 
+def test_calibration_library():
+    """bench.py's copy and MFMA-rate kernels: exported, and their argument checks answer before
+    any device work."""
+    cal = ctypes.CDLL(str(ROOT / "mrun_amd" / "lib" / "libmrun_calib.so"))
+    for n in ("mrun_calib_copy", "mrun_calib_read", "mrun_calib_read_threads", "mrun_calib_mfma",
+              "mrun_calib_mfma_chains"):
+        assert hasattr(cal, n), n
+    assert cal.mrun_calib_mfma_chains() == 4
+    cal.mrun_calib_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                    ctypes.c_void_p]
+    cal.mrun_calib_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    assert cal.mrun_calib_copy(FAKE + 8, FAKE, 64, None) != 0    # misaligned
+    assert cal.mrun_calib_copy(FAKE, FAKE, 24, None) != 0        # not whole 16-byte units
+    assert cal.mrun_calib_copy(FAKE, FAKE, 0, None) == 0         # nothing to copy
+    cal.mrun_calib_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                    ctypes.c_void_p]
+    assert cal.mrun_calib_read(FAKE + 4, 64, FAKE, None) != 0   # misaligned
+    assert cal.mrun_calib_read_threads() == 256 * 16 * 256
+    assert cal.mrun_calib_mfma(0, 8, FAKE, None) != 0
+    assert cal.mrun_calib_mfma(8, 1 << 17, FAKE, None) != 0
+
+
 FAKE = 1 << 20  # a 16-byte aligned address no check dereferences
 
 
