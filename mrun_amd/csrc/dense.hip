@@ -3,10 +3,15 @@
 // R(y + bias). Both products read the same x, so they run as one launch (the gate is one more
 // column block).
 //
-// Workgroup tile 64 rows x 64 columns, 4 waves of 32 x 32 (v_mfma_f32_32x32x16_bf16), K steps of
-// 64. The loop is latency-bound (a K step is 4 MFMAs per wave), so each thread keeps NST K steps
-// of loads in flight in registers (a ring unrolled by NST) and the LDS tiles are double-buffered:
-// one barrier per K step, which waits for LDS only, so the loads stay in flight across it.
+// Workgroup tile 64 rows x 64 columns, K steps of 64, v_mfma_f32_32x32x16_bf16. KG groups of 4
+// waves split K into KG consecutive ranges; each group stages its own range through its own
+// double-buffered LDS tiles (no operand is read twice), each wave of a group owns 32 x 32 of the
+// tile, and at the end the groups' partial sums meet in LDS and are added in group order. The
+// router's products are small (T x 257 outputs: a few hundred workgroups at most, one per CU),
+// so the K steps wait on load latency: the groups put KG waves on each SIMD and shorten the chain
+// of dependent steps KG times. Each thread keeps NST K steps of loads in flight in registers (a
+// ring unrolled by NST); one barrier per K step, which waits for LDS only, so the loads stay in
+// flight across it.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -23,13 +28,16 @@ struct Stage {
     uint4 a0, a1, b0, b1;
 };
 
-template <int NST>
-__global__ __launch_bounds__(256) void dense_gemm_kernel(DenseJob j) {
-    __shared__ __align__(16) bf16_t As[2][DBM * DLDK];
-    __shared__ __align__(16) bf16_t Bs[2][DBN * DLDK];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+template <int NST, int KG>
+__global__ __launch_bounds__(256 * KG) void dense_gemm_kernel(DenseJob j) {
+    // per group: A and B tiles, double-buffered; after the K loop the first KG - 1 groups' 4 x 64
+    // x 16 partial sums reuse the space (KG - 1 groups x 16 KB <= KG x 36 KB)
+    __shared__ __align__(16) bf16_t stage_lds[KG][2][2][DBM * DLDK];
+    const int kg = threadIdx.x >> 8, tid = threadIdx.x & 255, lane = tid & 63, wave = tid >> 6;
+    bf16_t(*As)[DBM * DLDK] = stage_lds[kg][0];
+    bf16_t(*Bs)[DBN * DLDK] = stage_lds[kg][1];
     if (j.zero && blockIdx.x == 0 && blockIdx.y == 0)
-        for (int i = tid; i < j.n_zero; i += 256) j.zero[i] = 0;
+        for (int i = threadIdx.x; i < j.n_zero; i += 256 * KG) j.zero[i] = 0;
 
     // column block -> weight (W0's blocks first, then W1's)
     const int nb0 = (j.N0 + DBN - 1) / DBN;
@@ -42,13 +50,13 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(DenseJob j) {
     const int n0 = (second ? (int)blockIdx.y - nb0 : (int)blockIdx.y) * DBN;
     const int row0 = blockIdx.x * DBM;
     const int mrows = min(DBM, j.M - row0);
-    const int K = j.K, nks = K / DBK;
+    const int K = j.K, nks = K / DBK / KG;  // K steps of each group (K a multiple of 64 KG)
 
     // staging: row tid / 4, 16 elements from k = 16 (tid % 4); rows past the end load the last
     // row (never stored)
     const int sr = tid >> 2, sk = (tid & 3) * 16;
-    const bf16_t *ap = j.A + (size_t)(row0 + min(sr, mrows - 1)) * j.lda + sk;
-    const bf16_t *bp = W + (size_t)min(n0 + sr, N - 1) * K + sk;
+    const bf16_t *ap = j.A + (size_t)(row0 + min(sr, mrows - 1)) * j.lda + sk + kg * nks * DBK;
+    const bf16_t *bp = W + (size_t)min(n0 + sr, N - 1) * K + sk + kg * nks * DBK;
     // stages pass by value (a reference into them would put the ring in scratch)
     auto load = [&](int ks) __attribute__((always_inline)) -> Stage {
         const uint4 *pa = (const uint4 *)(ap + ks * DBK), *pb = (const uint4 *)(bp + ks * DBK);
@@ -95,6 +103,20 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(DenseJob j) {
     for (int i = 0; i < NST - 1; ++i)
         if (ks + i < nks) ring[i] = step(ks + i, ring[i]);
 
+    if (KG > 1) {  // group g > 0 leaves its sums in LDS; group 0 adds them in group order
+        float *red = (float *)&stage_lds[0][0][0][0];
+        __syncthreads();
+        if (kg > 0) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) red[(((kg - 1) * 4 + wave) * 16 + i) * 64 + lane] = acc[i];
+        }
+        __syncthreads();
+        if (kg > 0) return;
+#pragma unroll
+        for (int g = 0; g < KG - 1; ++g)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[i] += red[((g * 4 + wave) * 16 + i) * 64 + lane];
+    }
     const int col = n0 + wn * 32 + fr;
     const float bv = (bias && col < N) ? bf2f(bias[col]) : 0.f;
 #pragma unroll
@@ -112,13 +134,21 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(DenseJob j) {
 
 bool dense_gemm_supported(int M, int K) { return M > 16 && K % DBK == 0 && K >= DBK; }
 
+// K groups of the launch: 2 measured best in the configs[2] prefill (router stage 18.0 against
+// 19.3 us with 1 group, 19.2 and 20.6 with 4 groups of 2- and 3-step rings) and with x in the
+// last-level cache (10.9 against 11.8 us, 4 groups 10.8); the steps wait on load latency, which
+// more waves per SIMD shorten only a little.
+constexpr int kDenseKG = 2;
+
 hipError_t launch_dense_gemm(const DenseJob &j, hipStream_t stream) {
     if (!dense_gemm_supported(j.M, j.K) || j.N0 <= 0 || (j.W1 && j.N1 <= 0))
         return hipErrorInvalidValue;
     const int nb = (j.N0 + DBN - 1) / DBN + (j.W1 ? (j.N1 + DBN - 1) / DBN : 0);
     dim3 grid((j.M + DBM - 1) / DBM, nb);
-    // a deeper ring (4, 6, 8 steps) measured no faster: the steps are not bound by load latency
-    dense_gemm_kernel<3><<<grid, 256, 0, stream>>>(j);
+    // a deeper ring (4, 6, 8 steps) measured no faster
+    if (j.K % (DBK * kDenseKG) == 0)
+        dense_gemm_kernel<3, kDenseKG><<<grid, 256 * kDenseKG, 0, stream>>>(j);
+    else dense_gemm_kernel<3, 1><<<grid, 256, 0, stream>>>(j);
     return hipGetLastError();
 }
 
