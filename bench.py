@@ -10,7 +10,8 @@ launch stream), this box's measured copy and MFMA rates beside the published pea
 restatement timed on a bounded sample on this host (all cores, and one thread).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens T] [--no-cpu] [--no-prefill]
-                    [--no-stack] [--no-coder] [--stack-only] [--prefill-only] [--coder-only]
+                    [--no-stack] [--no-coder] [--no-machine] [--stack-only] [--prefill-only]
+                    [--coder-only]
 """
 from __future__ import annotations
 
@@ -405,6 +406,8 @@ def main(argv=None) -> int:
     ap.add_argument("--no-stack", action="store_true")
     ap.add_argument("--stack-layers", type=int, default=40)
     ap.add_argument("--no-coder", action="store_true")
+    ap.add_argument("--no-machine", action="store_true",
+                    help="skip the copy, read and MFMA calibration of the box")
     ap.add_argument("--coder-only", action="store_true",
                     help="only the configs[4] Coder-shaped block; prints its own JSON line")
     ap.add_argument("--stack-only", action="store_true",
@@ -489,8 +492,10 @@ def main(argv=None) -> int:
     stack = None if args.no_stack else stack_point(args, Q, M, synth, torch)
     coder = None if args.no_coder else coder_point(args, M, synth, torch)
 
-    print("[bench] copy and MFMA calibration", file=sys.stderr, flush=True)
-    machine = machine_point(torch)
+    machine = None
+    if not args.no_machine:
+        print("[bench] copy and MFMA calibration", file=sys.stderr, flush=True)
+        machine = machine_point(torch)
 
     cpu = None
     if not args.no_cpu:
