@@ -251,13 +251,15 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmJob j) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Quantized grouped GEMM, group size 64: workgroup tile 128 rows x 256 B rows (glu: 128 gate + 128
-// up columns), 8 waves as 2 (rows) x 4 (columns); each wave owns 64 rows x two 32-column
-// fragments, 16 MFMAs per K step of 64.
-//  - Every global load reads whole 128-byte lines, 8 lanes to a line: A per K step, the packed
-//    codes per 4 K steps (a "super-step": 128 bytes of a B row), scales and biases per 16 K steps
-//    (a "chunk": 32 bytes of a row each). They pass through registers into LDS; A is re-paired on
-//    the way, codes stay packed (XOR-swizzled 16-byte units so fragment reads are conflict-free).
+// Quantized grouped GEMM, group size 64: workgroup tile 64 WM rows x 256 B rows (glu: 128 gate +
+// 128 up columns), 4 WM waves as WM (rows) x 4 (columns); each wave owns 64 rows x two 32-column
+// fragments, 16 MFMAs per K step of 64. The launcher builds WM = 1: 64-row tiles of 4 waves, two
+// workgroups per CU.
+//  - Global loads: A per K step (128 bytes of a row, 8 lanes to a line), the packed codes per SS
+//    K steps (a "super-step": 32 SS bytes of a B row, 64 with SS = 2), scales and biases per 16 K
+//    steps (a "chunk": 32 bytes of a row each). They pass through registers into LDS; A is
+//    re-paired on the way, codes stay packed (XOR-swizzled 16-byte units so fragment reads are
+//    conflict-free).
 //  - Each lane expands the 32 codes of a fragment and K step in registers. The K step's k are
 //    assigned to MFMA slots so that lane half h, sub-step s holds code word 4h + s of the step;
 //    the A tile is written in the same order (k block w at position 16 (w % 4) + 8 (w / 4)).
