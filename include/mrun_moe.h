@@ -16,6 +16,10 @@
  *    mrun_last_error() on the same thread — the facade's Result<_, tensor::Error(String)>
  *    (nuvec.rs:18-38). A failed call enqueues no work.
  *  - One stream per caller thread; the library starts no threads (engine.rs:647-648).
+ *  - A token or row count of 0 is an empty batch, as the facade's ops take empty arrays: the call
+ *    checks its weights and configuration, enqueues no work and returns 0 (no pointer or
+ *    workspace is read). Negative counts are MRUN_ERR_INVALID. mrun_moe_permute needs at least one
+ *    pair (the reference sorts only when T*k >= 64, moe.rs:17, 64).
  *  - Numerics follow the reference's bf16 semantics: each op computes in f32 and rounds its output
  *    once to bf16 (round to nearest even); contractions accumulate in f32.
  */

@@ -516,7 +516,8 @@ int mrun_moe_forward(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t tok
                      mrun_bf16 *out, void *workspace, size_t workspace_bytes,
                      mrun_stream_t stream) {
     Status st = check_block(moe);
-    if (st.ok() && tokens <= 0) st = Err(MRUN_ERR_INVALID, "tokens must be positive");
+    if (st.ok() && tokens < 0) st = Err(MRUN_ERR_INVALID, "tokens must not be negative");
+    if (st.ok() && tokens == 0) return report(st);  // an empty batch: nothing to do
     if (st.ok()) st = check_ptr(x, "x");
     if (st.ok()) st = check_ptr(out, "out");
     if (st.ok()) st = check_ptr(workspace, "workspace");
@@ -532,7 +533,11 @@ int mrun_moe_forward_profiled(const mrun_sparse_moe *moe, const mrun_bf16 *x, in
                               mrun_stream_t stream, void **events, int32_t n_events,
                               int32_t *n_stages) {
     Status st = check_block(moe);
-    if (st.ok() && tokens <= 0) st = Err(MRUN_ERR_INVALID, "tokens must be positive");
+    if (st.ok() && tokens < 0) st = Err(MRUN_ERR_INVALID, "tokens must not be negative");
+    if (st.ok() && tokens == 0) {  // an empty batch: nothing to do, no stage
+        if (n_stages) *n_stages = 0;
+        return report(st);
+    }
     if (st.ok()) st = check_ptr(x, "x");
     if (st.ok()) st = check_ptr(out, "out");
     if (st.ok()) st = check_ptr(workspace, "workspace");
@@ -557,7 +562,8 @@ int mrun_moe_router(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t toke
                     mrun_bf16 *logits, mrun_bf16 *gates, uint32_t *ids, mrun_bf16 *scores,
                     void *workspace, size_t workspace_bytes, mrun_stream_t stream) {
     Status st = check_block(moe);
-    if (st.ok() && tokens <= 0) st = Err(MRUN_ERR_INVALID, "tokens must be positive");
+    if (st.ok() && tokens < 0) st = Err(MRUN_ERR_INVALID, "tokens must not be negative");
+    if (st.ok() && tokens == 0) return report(st);  // an empty batch: nothing to do
     if (st.ok()) st = check_ptr(x, "x");
     if (st.ok() && (!ids || !scores)) st = Err(MRUN_ERR_INVALID, "ids and scores are required");
     bf16_t *lg = logits;
@@ -612,6 +618,10 @@ int mrun_gather_qmm(const mrun_bf16 *x, int32_t x_rows, const mrun_quantized *w,
                     void *workspace, size_t workspace_bytes, mrun_stream_t stream) {
     (void)sorted_indices;  // the permute below orders any index list; sorted input stays put
     Status st;
+    if (w && n == 0 && x_rows >= 0) {  // no index: an empty result, nothing to do
+        st = check_quantized(w, "gather_qmm weight", w->experts, w->out, w->in);
+        return report(st);
+    }
     if (!w || !indices || x_rows <= 0 || n <= 0 || n % x_rows != 0)
         st = Err(MRUN_ERR_INVALID, "gather_qmm: n must be a positive multiple of x_rows");
     if (st.ok()) st = check_quantized(w, "gather_qmm weight", w->experts, w->out, w->in);
@@ -658,8 +668,9 @@ int mrun_gather_qmm(const mrun_bf16 *x, int32_t x_rows, const mrun_quantized *w,
 int mrun_quantized_matmul(const mrun_bf16 *x, int32_t rows, const mrun_quantized *w,
                           mrun_bf16 *out, mrun_stream_t stream) {
     Status st;
-    if (!w || rows <= 0) st = Err(MRUN_ERR_INVALID, "quantized_matmul: bad arguments");
+    if (!w || rows < 0) st = Err(MRUN_ERR_INVALID, "quantized_matmul: bad arguments");
     if (st.ok()) st = check_quantized(w, "quantized_matmul weight", 1, w->out, w->in);
+    if (st.ok() && rows == 0) return report(st);  // an empty batch: nothing to do
     if (st.ok()) st = check_ptr(x, "x");
     if (st.ok()) st = check_ptr(out, "out");
     if (st.ok()) st = tensor::quantized_matmul(x, rows, *w, out, (hipStream_t)stream);
@@ -669,11 +680,12 @@ int mrun_quantized_matmul(const mrun_bf16 *x, int32_t rows, const mrun_quantized
 int mrun_linear_forward(const mrun_linear *l, const mrun_bf16 *x, int32_t rows, mrun_bf16 *out,
                         mrun_stream_t stream) {
     Status st;
-    if (!l || rows <= 0) st = Err(MRUN_ERR_INVALID, "linear: bad arguments");
+    if (!l || rows < 0) st = Err(MRUN_ERR_INVALID, "linear: bad arguments");
     if (st.ok() && l->weight) st = check_ptr(l->weight, "weight");
     if (st.ok() && !l->weight) st = check_quantized(&l->q, "linear weight", 1, l->out, l->in);
     if (st.ok() && l->weight && (l->out <= 0 || l->in <= 0))
         st = Err(MRUN_ERR_INVALID, "linear: bad shape");
+    if (st.ok() && rows == 0) return report(st);  // an empty batch: nothing to do
     if (st.ok()) st = check_ptr(x, "x");
     if (st.ok()) st = check_ptr(out, "out");
     if (st.ok()) st = tensor::linear(x, rows, *l, out, (hipStream_t)stream);
@@ -695,10 +707,11 @@ int mrun_moe_combine(const mrun_bf16 *y, const uint32_t *inverse, const mrun_bf1
                      int32_t tokens, int32_t top_k, int32_t hidden, const mrun_bf16 *shared_y,
                      const mrun_bf16 *shared_logit, mrun_bf16 *out, mrun_stream_t stream) {
     Status st;
-    if (tokens <= 0 || top_k <= 0 || hidden <= 0 || hidden % 8 != 0)
+    if (tokens < 0 || top_k <= 0 || hidden <= 0 || hidden % 8 != 0)
         st = Err(MRUN_ERR_INVALID, "combine: bad shape (hidden must be a multiple of 8)");
     else if (top_k > 16)
         st = Err(MRUN_ERR_UNSUPPORTED, "combine: top_k above 16");
+    if (st.ok() && tokens == 0) return report(st);  // an empty batch: nothing to do
     if (st.ok()) st = check_ptr(y, "y");
     if (st.ok() && !scores) st = Err(MRUN_ERR_INVALID, "scores is null");
     if (st.ok() && shared_y) st = check_ptr(shared_y, "shared_y");
@@ -728,7 +741,8 @@ int mrun_moe_stack_forward(const mrun_sparse_moe *layers, int32_t n_layers,
         if (st.ok() && std::memcmp(&layers[l].cfg, &layers[0].cfg, sizeof(mrun_moe_config)) != 0)
             st = Err(MRUN_ERR_INVALID, "stack: layers must share one config");
     }
-    if (st.ok() && tokens <= 0) st = Err(MRUN_ERR_INVALID, "tokens must be positive");
+    if (st.ok() && tokens < 0) st = Err(MRUN_ERR_INVALID, "tokens must not be negative");
+    if (st.ok() && tokens == 0) return report(st);  // an empty batch: nothing to do
     if (st.ok()) st = check_ptr(x, "x");
     if (st.ok()) st = check_ptr(workspace, "workspace");
     const mrun_moe_config &c = layers[0].cfg;
@@ -771,8 +785,9 @@ int mrun_moe_stack_forward(const mrun_sparse_moe *layers, int32_t n_layers,
 int mrun_rms_norm(const mrun_bf16 *x, const mrun_bf16 *w, int32_t rows, int32_t hidden, float eps,
                   mrun_bf16 *out, mrun_stream_t stream) {
     Status st;
-    if (rows <= 0 || hidden <= 0 || hidden % 8 != 0)
+    if (rows < 0 || hidden <= 0 || hidden % 8 != 0)
         st = Err(MRUN_ERR_INVALID, "rms_norm: bad shape (hidden must be a multiple of 8)");
+    if (st.ok() && rows == 0) return report(st);  // an empty batch: nothing to do
     if (st.ok()) st = check_ptr(x, "x");
     if (st.ok()) st = check_ptr(out, "out");
     if (st.ok() && x == out) st = Err(MRUN_ERR_INVALID, "rms_norm: out must not alias x");
@@ -787,8 +802,9 @@ int mrun_add_rms_norm(const mrun_bf16 *x, const mrun_bf16 *residual, const mrun_
                       int32_t rows, int32_t hidden, float eps, mrun_bf16 *h, mrun_bf16 *y,
                       mrun_stream_t stream) {
     Status st;
-    if (rows <= 0 || hidden <= 0 || hidden % 8 != 0)
+    if (rows < 0 || hidden <= 0 || hidden % 8 != 0)
         st = Err(MRUN_ERR_INVALID, "add_rms_norm: bad shape (hidden must be a multiple of 8)");
+    if (st.ok() && rows == 0) return report(st);  // an empty batch: nothing to do
     if (st.ok()) st = check_ptr(x, "x");
     if (st.ok()) st = check_ptr(residual, "residual");
     if (st.ok()) st = check_ptr(h, "h");

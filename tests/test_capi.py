@@ -149,7 +149,7 @@ def test_workspace_contract():
     assert rc == _lib.MRUN_ERR_WORKSPACE and "workspace" in lib.mrun_last_error().decode()
     rc = lib.mrun_moe_forward(ctypes.byref(m), FAKE, 1, FAKE, FAKE * 4, sizes[0], None)
     assert rc == _lib.MRUN_ERR_INVALID and "alias" in lib.mrun_last_error().decode()
-    rc = lib.mrun_moe_forward(ctypes.byref(m), FAKE, 0, FAKE * 2, FAKE * 4, sizes[0], None)
+    rc = lib.mrun_moe_forward(ctypes.byref(m), FAKE, -1, FAKE * 2, FAKE * 4, sizes[0], None)
     assert rc == _lib.MRUN_ERR_INVALID
 
 
@@ -162,3 +162,39 @@ def test_op_argument_errors():
     w = q(4, 64, 100)
     rc = lib.mrun_gather_qmm(FAKE, 2, ctypes.byref(w), FAKE, 4, 0, FAKE, FAKE, 1 << 20, None)
     assert rc == _lib.MRUN_ERR_INVALID and "scale groups" in lib.mrun_last_error().decode()
+
+
+def test_empty_batches_are_no_ops():
+    """A token or row count of 0 is an empty batch (the facade's ops take empty arrays): the call
+    checks its weights and returns 0 without reading a pointer; negative counts are refused."""
+    lib = _lib.load()
+    m = block()
+    assert lib.mrun_moe_forward(ctypes.byref(m), None, 0, None, None, 0, None) == 0
+    assert lib.mrun_moe_forward(ctypes.byref(m), FAKE, -1, FAKE * 2, FAKE * 4, 1 << 30,
+                                None) == _lib.MRUN_ERR_INVALID
+    n_stages = ctypes.c_int32(7)
+    assert lib.mrun_moe_forward_profiled(ctypes.byref(m), None, 0, None, None, 0, None, None, 0,
+                                         ctypes.byref(n_stages)) == 0
+    assert n_stages.value == 0
+    assert lib.mrun_moe_router(ctypes.byref(m), None, 0, None, None, None, None, None, 0,
+                               None) == 0
+    # the weights are still checked
+    bad = block(E=4, k=8)
+    assert lib.mrun_moe_forward(ctypes.byref(bad), None, 0, None, None, 0,
+                                None) == _lib.MRUN_ERR_INVALID
+    w = q(4, 64, 128)
+    assert lib.mrun_gather_qmm(None, 0, ctypes.byref(w), None, 0, 0, None, None, 0, None) == 0
+    assert lib.mrun_gather_qmm(None, 0, ctypes.byref(q(4, 64, 100)), None, 0, 0, None, None, 0,
+                               None) == _lib.MRUN_ERR_INVALID
+    assert lib.mrun_quantized_matmul(None, 0, ctypes.byref(q(1, 64, 128)), None, None) == 0
+    assert lib.mrun_quantized_matmul(None, -2, ctypes.byref(q(1, 64, 128)), None,
+                                     None) == _lib.MRUN_ERR_INVALID
+    lin = Linear(FAKE, Quantized(), None, 64, 128)
+    assert lib.mrun_linear_forward(ctypes.byref(lin), None, 0, None, None) == 0
+    assert lib.mrun_moe_combine(None, None, None, 0, 8, 2048, None, None, None, None) == 0
+    assert lib.mrun_rms_norm(None, None, 0, 2048, 1e-6, None, None) == 0
+    assert lib.mrun_add_rms_norm(None, None, None, 0, 2048, 1e-6, None, None, None) == 0
+    assert lib.mrun_rms_norm(None, None, -1, 2048, 1e-6, None, None) == _lib.MRUN_ERR_INVALID
+    layers = (SparseMoe * 2)(m, m)
+    assert lib.mrun_moe_stack_forward(layers, 2, None, 1e-6, None, 0, None, 0, None) == 0
+    assert lib.mrun_moe_workspace_bytes(ctypes.byref(m.cfg), 0) == 0

@@ -257,6 +257,18 @@ def test_rows_keep_their_one_row_bits(q_dev):
         assert np.array_equal(one[0], batch[t]), f"row {t}"
 
 
+def test_empty_batch(q_dev):
+    """T = 0: the block, the router and the stack return empty results and enqueue nothing."""
+    x = torch.empty(0, Q.hidden, dtype=torch.bfloat16, device="cuda")
+    out = q_dev.forward(x)
+    logits, gates, ids, scores = q_dev.router_forward(x)
+    st = M.MoeStack([q_dev, q_dev], None, 1e-6)
+    st.forward_(x)
+    torch.cuda.synchronize()
+    assert tuple(out.shape) == (0, Q.hidden)
+    assert tuple(ids.shape) == (0, Q.top_k) and tuple(logits.shape) == (0, Q.experts)
+
+
 def test_forward_is_deterministic(q_dev):
     x = M.bf16_tensor(synth.make_x(Q, 512, config=synth.CFG_DECODE, layer=5))
     a = M.bf16_bits(q_dev.forward(x))
