@@ -6,8 +6,10 @@ synthetic seeded data, decode T = 1. A step is one block forward over the batch.
 also carries the T = 2, 4, 16 decode sweep, the configs[2] prefill (T = 2048, Zipf-skewed
 router), the configs[3] stack of 40 layers (T = 1 and T = 4096) and the configs[4] Coder-shaped
 block (T = 1, 8, 8192) measured the same way, the dominant kernel's roofline (HIP events on the
-launch stream), this box's measured copy and MFMA rates beside the published peaks, and the CPU
-restatement timed on a bounded sample on this host (all cores, and one thread).
+launch stream), this box's measured copy and MFMA rates beside the published peaks, each decode
+point also timed with the 256 MB last-level cache flushed before every forward (`cold_*`: the
+repeated forward keeps the 17 MB block in that cache), and the CPU restatement timed on a bounded
+sample on this host (all cores, and one thread).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens T] [--no-cpu] [--no-prefill]
                     [--no-stack] [--no-coder] [--no-machine] [--stack-only] [--prefill-only]
@@ -197,11 +199,7 @@ def cpu_baseline(hb, x_np, seconds: float, seconds_1t: float = 4.0):
                                      f"{med1 * 1e6:.0f}"}}
 
 
-def machine_point(torch) -> dict:
-    """This box's roofline denominators beside the published peaks: a 4 GiB read (larger than the
-    256 MB last-level cache), a 1 GiB device copy (bytes read + written per second) and
-    back-to-back v_mfma_f32_32x32x16_bf16 on every SIMD (flop/s), all with kernels of
-    libmrun_calib.so timed by HIP events on the launch stream."""
+def calib_lib():
     root = os.path.dirname(os.path.abspath(__file__))
     lib = ctypes.CDLL(os.path.join(root, "mrun_amd", "lib", "libmrun_calib.so"))
     lib.mrun_calib_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
@@ -209,6 +207,43 @@ def machine_point(torch) -> dict:
     lib.mrun_calib_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     lib.mrun_calib_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
                                     ctypes.c_void_p]
+    return lib
+
+
+class ColdTimer:
+    """HIP-event time of single forwards, each after a 1 GiB read that pushes the block's weights
+    out of the 256 MB last-level cache (the repeated-forward loop keeps a 17 MB block in it)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.lib = calib_lib()
+        self.buf = torch.ones((1 << 30) // 4, dtype=torch.int32, device="cuda")
+        self.rout = torch.empty(self.lib.mrun_calib_read_threads(), dtype=torch.int32,
+                                device="cuda")
+
+    def time(self, dev, x, n: int) -> float:
+        stream = self.torch.cuda.current_stream()
+        sp = ctypes.c_void_p(stream.cuda_stream)
+        out = self.torch.empty_like(x)
+        ws = dev.workspace(x.shape[0])
+        ev = Events(2)
+        tot = 0.0
+        for _ in range(n):
+            assert self.lib.mrun_calib_read(self.buf.data_ptr(), 1 << 30, self.rout.data_ptr(),
+                                            sp) == 0
+            ev.record(0, stream)
+            dev.forward(x, out=out, workspace=ws)
+            ev.record(1, stream)
+            tot += ev.ms(0, 1)
+        return tot / n
+
+
+def machine_point(torch) -> dict:
+    """This box's roofline denominators beside the published peaks: a 4 GiB read (larger than the
+    256 MB last-level cache), a 1 GiB device copy (bytes read + written per second) and
+    back-to-back v_mfma_f32_32x32x16_bf16 on every SIMD (flop/s), all with kernels of
+    libmrun_calib.so timed by HIP events on the launch stream."""
+    lib = calib_lib()
     stream = torch.cuda.current_stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
     ev = Events(2)
@@ -407,7 +442,8 @@ def main(argv=None) -> int:
     ap.add_argument("--stack-layers", type=int, default=40)
     ap.add_argument("--no-coder", action="store_true")
     ap.add_argument("--no-machine", action="store_true",
-                    help="skip the copy, read and MFMA calibration of the box")
+                    help="skip the copy, read and MFMA calibration of the box and the decode "
+                         "timings with the last-level cache flushed")
     ap.add_argument("--coder-only", action="store_true",
                     help="only the configs[4] Coder-shaped block; prints its own JSON line")
     ap.add_argument("--stack-only", action="store_true",
@@ -450,12 +486,15 @@ def main(argv=None) -> int:
     hb = synth.make_block(Q, config=synth.CFG_DECODE)
     dev = M.SparseMoe(hb)
 
+    cold = None if args.no_machine else ColdTimer(torch)
+
     def decode_point(T, steps, warmup):
         x_np = synth.make_x(Q, T, config=synth.CFG_DECODE, layer=T)
         x = M.bf16_tensor(x_np)
         _, _, ids, _ = dev.router_forward(x)
         n_active = int(np.unique(M.u32_array(ids)).size)
         wall, dev_ms, _ = time_forward(dev, x, steps, warmup, torch)
+        cold_ms = cold.time(dev, x, 30) if cold else None
         stages = time_stages(dev, x, 50, torch)
         try:
             g_ms, _ = time_graph(dev, x, steps, torch)
@@ -464,7 +503,7 @@ def main(argv=None) -> int:
             g_ms = None
         b = decode_bytes(Q, n_active, T)
         return {"tokens": T, "n_active": n_active, "ms_per_step": wall, "device_ms": dev_ms,
-                "graph_ms": g_ms, "tokens_per_s": T / (wall * 1e-3),
+                "cold_device_ms": cold_ms, "graph_ms": g_ms, "tokens_per_s": T / (wall * 1e-3),
                 "stages_us": stages, "bytes": b,
                 "block_hbm_frac": b["block"] / (dev_ms * 1e-3) / HBM_PEAK}, x_np
 
@@ -521,6 +560,8 @@ def main(argv=None) -> int:
                    "weights": "4-bit affine, group 64, bf16 scales/biases",
                    "tokens": args.tokens},
         "us_per_layer": main_pt["device_ms"] * 1e3,
+        "cold_us_per_layer": (main_pt["cold_device_ms"] * 1e3 if main_pt["cold_device_ms"]
+                              else None),
         "graph_us_per_layer": main_pt["graph_ms"] * 1e3 if main_pt["graph_ms"] else None,
         "block_hbm_frac": main_pt["block_hbm_frac"],
         "stages_us": main_pt["stages_us"],
