@@ -729,9 +729,10 @@ hipError_t launch_decode(const DecodeJob &j, hipStream_t s, StageMarks *marks) {
     if (marks) marks->mark(s);
 
     const int n_ch = j.D >> 5;
-    // rows per wave: about 1024 routed waves-of-rows at T = 1, 2 and 4 (8, 16, 32 expert slots)
-    // rows wider than 2048 take one row per wave and the streaming loop at every T
-    const int rg = (j.T == 1 || n_ch > 64) ? 1 : (j.T == 2 ? 2 : 4);
+    // rows per wave: 2 at T = 1 and 2 (512 and 1024 routed waves-of-rows over 8 and 16 expert
+    // slots; at T = 1 one row measured 18.9 us per block, two 18.3, four 19.5), 4 above; rows
+    // wider than 2048 take one row per wave and the streaming loop at every T
+    const int rg = n_ch > 64 ? 1 : (j.T <= 2 ? 2 : 4);
     // 4 waves per workgroup: 8 and 16 (fewer redundant top-ks per CU) measured slower
     if (rg == 1) launch_k2<1, 4>(j, n_ch, s);
     else if (rg == 2) launch_k2<2, 4>(j, n_ch, s);
