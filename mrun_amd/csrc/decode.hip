@@ -10,7 +10,7 @@
 //                expert's gate/up rows for its pairs. The first routed workgroup publishes the
 //                routing for K3.
 //   K3 down    : prefetches the shared expert's down rows, reads the routing, computes the routed
-//                down rows of every active expert for its 4 output rows, then the combine:
+//                down rows of every active expert for its 4 or 8 output rows, then the combine:
 //                out = R(R(sum_j R(y[t,j] * s[t,j])) + R(R(sigmoid(g_t)) * shared[t])).
 // Rows wider than 2048 (the Coder shape): a K2 workgroup streams several row blocks pair by pair
 // with the next rows loaded before the current ones are computed, and without a shared expert K3
@@ -688,10 +688,13 @@ static void launch_k2(DecodeJob j, int n_ch, hipStream_t s) {
 
 template <int LPR, int CPL>
 static void launch_k3_s(const DecodeJob &j, hipStream_t s) {
-    // 4 output rows per workgroup; pairs per load batch keep a batch's activations and weight rows
+    // output rows per workgroup: two row groups per wave, at least 4 rows (8 with 16-lane rows,
+    // where 4, 16 and 32 measured slower: T = 1 18.3, 18.1, 20.7 against 17.4 us per block; fewer
+    // workgroups re-read the pairs' activation rows fewer times, until each wave's chain of pair
+    // batches grows too long). Pairs per load batch keep a batch's activations and weight rows
     // within ~128 registers, and are no more than a wave's pairs (a wave takes ceil(P / 4) pairs;
     // slots past them would load their last pair again)
-    constexpr int DR = 4;
+    constexpr int DR = 2 * (64 / LPR) > 4 ? 2 * (64 / LPR) : 4;
     constexpr int NRG = DR / (64 / LPR) > 0 ? DR / (64 / LPR) : 1;
     constexpr int PB = (NRG * CPL <= 2) ? 4 : (NRG * CPL <= 4 ? 2 : 1);
     if (PB == 4 && (j.T * j.k + 3) / 4 <= 2) launch_k3_pb<LPR, CPL, 2, DR>(j, s);
