@@ -112,6 +112,15 @@ int mrun_moe_forward_profiled(const mrun_sparse_moe *moe, const mrun_bf16 *x, in
                               int32_t *n_stages);
 const char *mrun_moe_stage_names(const mrun_moe_config *cfg, int32_t tokens);
 
+/* mrun_moe_forward with the decode gate/up kernel timed by its own launch (benchmark
+ * instrumentation; no counterpart in the reference): start_event and stop_event, hipEvent_t
+ * handles created by the caller, are updated by that launch at the kernel's start and end
+ * (hipExtLaunchKernel), so their elapsed time is the kernel's duration without launch gaps. A
+ * batch that runs the prefill schedule has no such launch and leaves the events untouched. */
+int mrun_moe_forward_timed(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t tokens,
+                           mrun_bf16 *out, void *workspace, size_t workspace_bytes,
+                           mrun_stream_t stream, void *start_event, void *stop_event);
+
 /* The router of SparseMoe::forward (moe.rs:151-159): logits = gate.forward(x) (load.rs:294-306),
  * gates = softmax(logits, precise) (nuvec.rs:593-598), ids = the top-k of argpartition + slice
  * (nuvec.rs:558-562, 313-316; equal gates rank the lower id first, ids listed by rank), scores =

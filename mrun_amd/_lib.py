@@ -82,6 +82,11 @@ SIGNATURES = {
          POINTER(c_void_p), c_int32, POINTER(c_int32)],
     ),
     "mrun_moe_stage_names": (c_char_p, [POINTER(MoeConfig), c_int32]),
+    "mrun_moe_forward_timed": (
+        c_int32,
+        [POINTER(SparseMoe), c_void_p, c_int32, c_void_p, c_void_p, c_size_t, c_void_p,
+         c_void_p, c_void_p],
+    ),
     "mrun_moe_router": (
         c_int32,
         [POINTER(SparseMoe), c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p,

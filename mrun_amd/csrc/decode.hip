@@ -17,6 +17,8 @@
 // takes one wave per pair streaming that expert's down rows. Every row keeps the same bits.
 // Pair p = t*k + j indexes the activations (act [T*k, I]), so no argsort is needed at decode; the
 // results are the same as the sorted dispatch's, row by row.
+#include <hip/hip_ext.h>
+
 #include "common.hpp"
 #include "gemv_core.hpp"
 #include "kernels.hpp"
@@ -666,15 +668,22 @@ static void launch_k3_pb(const DecodeJob &j, hipStream_t s);
 // row blocks at T = 1 to 16; caps of 512, 2048 and 4096 per token measured slower.) Narrower rows
 // (one round already) take one row block per workgroup (the loop measured slower there).
 template <int RG, int NW, bool LOOP>
-static void launch_k2_l(const DecodeJob &j, int n_ch, dim3 g2, hipStream_t s) {
-    if (n_ch <= 64) decode_gateup_kernel<64, 1, RG, NW, LOOP><<<g2, 64 * NW, 0, s>>>(j);
-    else if (n_ch <= 128) decode_gateup_kernel<64, 2, RG, NW, LOOP><<<g2, 64 * NW, 0, s>>>(j);
-    else if (n_ch <= 192) decode_gateup_kernel<64, 3, RG, NW, LOOP><<<g2, 64 * NW, 0, s>>>(j);
-    else decode_gateup_kernel<64, 4, RG, NW, LOOP><<<g2, 64 * NW, 0, s>>>(j);
+static void launch_k2_l(const DecodeJob &j, int n_ch, dim3 g2, hipStream_t s,
+                        const StageMarks *marks) {
+    auto go = [&](auto kernel) {
+        if (marks && marks->k2_start)  // timed by the launch itself (benchmark instrumentation)
+            hipExtLaunchKernelGGL(kernel, g2, dim3(64 * NW), 0, s, marks->k2_start, marks->k2_stop,
+                                  0, j);
+        else kernel<<<g2, 64 * NW, 0, s>>>(j);
+    };
+    if (n_ch <= 64) go(decode_gateup_kernel<64, 1, RG, NW, LOOP>);
+    else if (n_ch <= 128) go(decode_gateup_kernel<64, 2, RG, NW, LOOP>);
+    else if (n_ch <= 192) go(decode_gateup_kernel<64, 3, RG, NW, LOOP>);
+    else go(decode_gateup_kernel<64, 4, RG, NW, LOOP>);
 }
 
 template <int RG, int NW>
-static void launch_k2(DecodeJob j, int n_ch, hipStream_t s) {
+static void launch_k2(DecodeJob j, int n_ch, hipStream_t s, const StageMarks *marks) {
     const int per_slot = j.I / (NW * RG), sh_blocks = j.S / (NW * RG);
     int L = 1;
     while (RG == 1 && n_ch > 64 && j.max_slots * per_slot / L > 1024 * j.T &&
@@ -682,8 +691,8 @@ static void launch_k2(DecodeJob j, int n_ch, hipStream_t s) {
         L *= 2;
     j.gu_loop = L;
     dim3 g2(shared_gateup_blocks(j, NW * RG * L) + (j.I / (NW * RG * L)) * j.max_slots);
-    if (RG == 1 && L > 1) launch_k2_l<1, NW, true>(j, n_ch, g2, s);
-    else launch_k2_l<RG, NW, false>(j, n_ch, g2, s);
+    if (RG == 1 && L > 1) launch_k2_l<1, NW, true>(j, n_ch, g2, s, marks);
+    else launch_k2_l<RG, NW, false>(j, n_ch, g2, s, marks);
 }
 
 template <int LPR, int CPL>
@@ -737,9 +746,9 @@ hipError_t launch_decode(const DecodeJob &j, hipStream_t s, StageMarks *marks) {
     // wider than 2048 take one row per wave and the streaming loop at every T
     const int rg = n_ch > 64 ? 1 : (j.T <= 2 ? 2 : 4);
     // 4 waves per workgroup: 8 and 16 (fewer redundant top-ks per CU) measured slower
-    if (rg == 1) launch_k2<1, 4>(j, n_ch, s);
-    else if (rg == 2) launch_k2<2, 4>(j, n_ch, s);
-    else launch_k2<4, 4>(j, n_ch, s);
+    if (rg == 1) launch_k2<1, 4>(j, n_ch, s, marks);
+    else if (rg == 2) launch_k2<2, 4>(j, n_ch, s, marks);
+    else launch_k2<4, 4>(j, n_ch, s, marks);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (marks) marks->mark(s);

@@ -34,6 +34,9 @@ struct StageMarks {
     hipEvent_t *events = nullptr;
     int n_events = 0;
     int count = 0;
+    // optional: the decode gate/up launch records these itself at its start and end
+    // (hipExtLaunchKernel), so their elapsed time is that kernel's duration
+    hipEvent_t k2_start = nullptr, k2_stop = nullptr;
     void mark(hipStream_t s) {
         if (events && count + 1 < n_events) (void)hipEventRecord(events[count + 1], s);
         ++count;

@@ -552,6 +552,26 @@ int mrun_moe_forward_profiled(const mrun_sparse_moe *moe, const mrun_bf16 *x, in
     return report(st);
 }
 
+int mrun_moe_forward_timed(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t tokens,
+                           mrun_bf16 *out, void *workspace, size_t workspace_bytes,
+                           mrun_stream_t stream, void *start_event, void *stop_event) {
+    Status st = check_block(moe);
+    if (st.ok() && tokens < 0) st = Err(MRUN_ERR_INVALID, "tokens must not be negative");
+    if (st.ok() && tokens == 0) return report(st);  // an empty batch: nothing to do
+    if (st.ok()) st = check_ptr(x, "x");
+    if (st.ok()) st = check_ptr(out, "out");
+    if (st.ok()) st = check_ptr(workspace, "workspace");
+    if (st.ok() && x == out) st = Err(MRUN_ERR_INVALID, "out must not alias x");
+    if (st.ok() && (!start_event || !stop_event))
+        st = Err(MRUN_ERR_INVALID, "forward_timed needs both events");
+    StageMarks marks;
+    marks.k2_start = (hipEvent_t)start_event, marks.k2_stop = (hipEvent_t)stop_event;
+    if (st.ok())
+        st = models::sparse_moe_forward(*moe, x, tokens, out, (char *)workspace, workspace_bytes,
+                                        (hipStream_t)stream, &marks);
+    return report(st);
+}
+
 const char *mrun_moe_stage_names(const mrun_moe_config *cfg, int32_t tokens) {
     if (!cfg || tokens <= 0) return "";
     // for 4-bit experts (8-bit ones run the prefill stages at every token count)

@@ -8,6 +8,8 @@ broken the other way does not count as a numeric error.
 """
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -267,6 +269,27 @@ def test_empty_batch(q_dev):
     torch.cuda.synchronize()
     assert tuple(out.shape) == (0, Q.hidden)
     assert tuple(ids.shape) == (0, Q.top_k) and tuple(logits.shape) == (0, Q.experts)
+
+
+def test_timed_forward_matches_forward(q_dev):
+    """mrun_moe_forward_timed (the benchmark's kernel-timed forward) gives the plain forward's bits,
+    and its events bracket the decode gate/up kernel: a positive duration below the forward's."""
+    import bench
+    from mrun_amd import _lib
+
+    x = M.bf16_tensor(synth.make_x(Q, 1, config=synth.CFG_DECODE, layer=11))
+    ref = M.bf16_bits(q_dev.forward(x))
+    out = torch.empty_like(x)
+    ws = q_dev.workspace(1)
+    ev = bench.Events(2)
+    stream = torch.cuda.current_stream()
+    _lib.check(_lib.load().mrun_moe_forward_timed(
+        ctypes.byref(q_dev.c), ctypes.c_void_p(x.data_ptr()), 1, ctypes.c_void_p(out.data_ptr()),
+        ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(stream.cuda_stream),
+        ctypes.c_void_p(ev.ev[0]), ctypes.c_void_p(ev.ev[1])))
+    torch.cuda.synchronize()
+    assert np.array_equal(M.bf16_bits(out), ref)
+    assert 0.0 < ev.ms(0, 1) < 1.0  # milliseconds
 
 
 def test_forward_is_deterministic(q_dev):
