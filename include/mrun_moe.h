@@ -116,10 +116,20 @@ const char *mrun_moe_stage_names(const mrun_moe_config *cfg, int32_t tokens);
  * instrumentation; no counterpart in the reference): start_event and stop_event, hipEvent_t
  * handles created by the caller, are updated by that launch at the kernel's start and end
  * (hipExtLaunchKernel), so their elapsed time is the kernel's duration without launch gaps. A
- * batch that runs the prefill schedule has no such launch and leaves the events untouched. */
+ * batch that runs the prefill schedule has no such launch: the call returns MRUN_ERR_UNSUPPORTED
+ * and enqueues nothing. */
 int mrun_moe_forward_timed(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t tokens,
                            mrun_bf16 *out, void *workspace, size_t workspace_bytes,
                            mrun_stream_t stream, void *start_event, void *stop_event);
+
+/* Where a forward leaves its routing inside the caller's workspace (instrumentation for tests and
+ * profilers; no counterpart in the reference, whose intermediate arrays are not observable). For
+ * `tokens` rows, at[0..6) receive byte offsets into the workspace of: ids [tokens, k] u32 and
+ * scores [tokens, k] bf16 (the router's choice, moe.rs:151-159), and, for a batch that runs the
+ * prefill schedule (more than 16 tokens, or 8-bit or dense experts), the sorted dispatch of
+ * SwitchGlu::forward (moe.rs:65-75): offsets [experts + 1], order, inverse and token [tokens*k].
+ * They hold the last forward's values until the workspace is reused. */
+int mrun_moe_workspace_routing(const mrun_moe_config *cfg, int32_t tokens, size_t *at);
 
 /* The router of SparseMoe::forward (moe.rs:151-159): logits = gate.forward(x) (load.rs:294-306),
  * gates = softmax(logits, precise) (nuvec.rs:593-598), ids = the top-k of argpartition + slice
@@ -135,7 +145,9 @@ int mrun_moe_router(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t toke
  * nuvec.rs:554-556), inverse = argsort(order), token = floor_divide(order, k) (nuvec.rs:523-526).
  * ids [pairs] u32 with pairs = tokens*k; offsets [experts + 1] (expert e's sorted rows are
  * [offsets[e], offsets[e+1])), order, inverse, token [pairs]. Any output may be NULL except
- * offsets. */
+ * offsets. Ids must be below `experts` (others are skipped and leave their entries unwritten).
+ * The workspace holds per-block expert counts: mrun_moe_permute_workspace_bytes(pairs, experts)
+ * bytes. */
 int mrun_moe_permute(const uint32_t *ids, int32_t pairs, int32_t top_k, int32_t experts,
                      uint32_t *offsets, uint32_t *order, uint32_t *inverse, uint32_t *token,
                      void *workspace, size_t workspace_bytes, mrun_stream_t stream);

@@ -98,6 +98,7 @@ SIGNATURES = {
          c_size_t, c_void_p],
     ),
     "mrun_moe_permute_workspace_bytes": (c_size_t, [c_int32, c_int32]),
+    "mrun_moe_workspace_routing": (c_int32, [POINTER(MoeConfig), c_int32, POINTER(c_size_t)]),
     "mrun_gather_qmm": (
         c_int32,
         [c_void_p, c_int32, POINTER(Quantized), c_void_p, c_int32, c_int32, c_void_p, c_void_p,

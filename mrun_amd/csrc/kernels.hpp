@@ -66,22 +66,22 @@ struct PermuteOut {
 hipError_t launch_topk(const bf16_t *logits, int T, int E, int k, bool norm, bf16_t *gates,
                        uint32_t *ids, bf16_t *scores, hipStream_t stream);
 
-// Stable counting sort of ids [P] (values < E) by expert (one workgroup).
-hipError_t launch_permute(const uint32_t *ids, int P, int k, int E, const PermuteOut &out,
-                          hipStream_t stream);
+// The stable sort of ids [P] (values < E) by expert: order = argsort(ids) (stable), inverse,
+// token = order / k, offsets, and the active list and tiles when asked for (moe.rs:69-75). Two
+// launches: per-block expert counts into counts [permute_counts_words(P, E)], then the scatter.
+size_t permute_counts_words(int P, int E);
+hipError_t launch_permute(const uint32_t *ids, int P, int k, int E, uint32_t *counts,
+                          const PermuteOut &out, hipStream_t stream);
 
-// Prefill routing in two launches over many workgroups: top-k + per-workgroup histograms that
-// reserve ranges in counts[kRankSlots][E] (zero on entry) with one atomic per (workgroup, expert),
-// workgroup w using slot w % kRankSlots (one per XCD under round-robin dispatch, so workgroups of
-// different XCDs do not contend for one counter); then a scatter that places every pair inside its
-// expert's range (slot ranges in slot order). Rows of an expert are contiguous but not in token
-// order; every row's result is independent of its position.
-constexpr int kRankSlots = 8;
-hipError_t launch_topk_rank(const bf16_t *logits, int T, int E, int k, bool norm, uint32_t *ids,
-                            bf16_t *scores, uint32_t *counts, uint32_t *rank,
-                            hipStream_t stream);
-hipError_t launch_scatter(const uint32_t *ids, const uint32_t *rank, const uint32_t *counts,
-                          int P, int k, int E, const PermuteOut &out, hipStream_t stream);
+// The forward's prefill routing in two launches: softmax + top-k of four tokens per workgroup,
+// whose expert histograms are added into counts [ceil(T / bt)][E] (zero on entry; bt =
+// route_block_tokens(k, E) tokens per block), then the same stable scatter as launch_permute.
+// Atomics only ever sum counts, so every output is deterministic and equals the stable argsort.
+int route_block_tokens(int k, int E);
+hipError_t launch_topk_count(const bf16_t *logits, int T, int E, int k, bool norm, uint32_t *ids,
+                             bf16_t *scores, uint32_t *counts, hipStream_t stream);
+hipError_t launch_route_scatter(const uint32_t *ids, const uint32_t *counts, int T, int k, int E,
+                                const PermuteOut &out, hipStream_t stream);
 
 // ---- products ----
 

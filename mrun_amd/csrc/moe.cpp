@@ -164,7 +164,8 @@ static Status check_block(const mrun_sparse_moe *m) {
 
 struct Plan {
     size_t logits, ids, scores, offsets, order, inverse, token, active, n_active, tiles, n_tiles;
-    size_t counts, rank;
+    size_t counts;
+    int n_counts;
     size_t act, y, sh_logit, sh_act, sh_y, total;
     int max_tiles;
 };
@@ -193,8 +194,10 @@ static Plan make_plan(const mrun_moe_config &c, int T) {
     p.n_active = take(4);
     p.tiles = take(12 * (size_t)p.max_tiles);
     p.n_tiles = take(4);
-    p.counts = take(4 * (size_t)kRankSlots * E);
-    p.rank = take(4 * P);
+    // per-block expert counts of the prefill routing (route_block_tokens tokens per block)
+    const int bt = route_block_tokens(c.top_k, c.experts);
+    p.n_counts = (int)(((size_t)T + bt - 1) / bt * E);
+    p.counts = take(4 * (size_t)p.n_counts);
     p.act = take(2 * P * I);
     p.y = take(2 * P * D);
     if (S > 0) {
@@ -396,7 +399,7 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
     }
 
     // prefill
-    uint32_t *counts = (uint32_t *)at(p.counts), *rank = (uint32_t *)at(p.rank);
+    uint32_t *counts = (uint32_t *)at(p.counts);
     if (m.gate.weight && (!S || m.shared_expert_gate.weight) && dense_gemm_supported(T, D)) {
         // router and shared gate: one launch over x
         DenseJob dj{};
@@ -406,22 +409,22 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
             dj.W1 = m.shared_expert_gate.weight, dj.bias1 = m.shared_expert_gate.bias;
             dj.N1 = 1, dj.out1 = sh_logit, dj.ldo1 = 1;
         }
-        dj.zero = counts, dj.n_zero = kRankSlots * E;
+        dj.zero = counts, dj.n_zero = p.n_counts;
         TRY_HIP(launch_dense_gemm(dj, s), "router (mfma)");
         st.mark(s);  // (the shared gate's stage below stays empty: it ran in this launch)
     } else {
-        TRY(tensor::linear(x, T, m.gate, logits, s, counts, kRankSlots * E));
+        TRY(tensor::linear(x, T, m.gate, logits, s, counts, p.n_counts));
         st.mark(s);
         if (S) TRY(tensor::linear(x, T, m.shared_expert_gate, sh_logit, s));
     }
     st.mark(s);
-    TRY_HIP(launch_topk_rank(logits, T, E, k, c.norm_topk_prob != 0, ids, scores, counts, rank, s),
+    TRY_HIP(launch_topk_count(logits, T, E, k, c.norm_topk_prob != 0, ids, scores, counts, s),
             "top-k");
     st.mark(s);
     PermuteOut pt = po;
     pt.tiles = (uint32_t *)at(p.tiles);
     pt.n_tiles = (uint32_t *)at(p.n_tiles);
-    TRY_HIP(launch_scatter(ids, rank, counts, P, k, E, pt, s), "scatter");
+    TRY_HIP(launch_route_scatter(ids, counts, T, k, E, pt, s), "scatter");
     st.mark(s);
     if (mfma) {
         GemmJob g{};
@@ -564,6 +567,10 @@ int mrun_moe_forward_timed(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32
     if (st.ok() && x == out) st = Err(MRUN_ERR_INVALID, "out must not alias x");
     if (st.ok() && (!start_event || !stop_event))
         st = Err(MRUN_ERR_INVALID, "forward_timed needs both events");
+    if (st.ok() && !models::is_decode(*moe, tokens))
+        st = Err(MRUN_ERR_UNSUPPORTED,
+                 "forward_timed: this batch runs the prefill schedule, which has no decode "
+                 "gate/up launch to time");
     StageMarks marks;
     marks.k2_start = (hipEvent_t)start_event, marks.k2_stop = (hipEvent_t)stop_event;
     if (st.ok())
@@ -601,36 +608,50 @@ int mrun_moe_router(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t toke
 }
 
 size_t mrun_moe_permute_workspace_bytes(int32_t pairs, int32_t experts) {
-    (void)pairs;
-    (void)experts;
-    return 0;
+    if (pairs <= 0 || experts <= 0 || experts > 1024) return 0;
+    return a256(4 * permute_counts_words(pairs, experts));
 }
 
 int mrun_moe_permute(const uint32_t *ids, int32_t pairs, int32_t top_k, int32_t experts,
                      uint32_t *offsets, uint32_t *order, uint32_t *inverse, uint32_t *token,
                      void *workspace, size_t workspace_bytes, mrun_stream_t stream) {
-    (void)workspace;
-    (void)workspace_bytes;
     Status st;
     if (!ids || !offsets) st = Err(MRUN_ERR_INVALID, "ids and offsets are required");
     else if (pairs <= 0 || top_k <= 0 || pairs % top_k != 0)
         st = Err(MRUN_ERR_INVALID, "pairs must be a positive multiple of top_k");
     else if (experts <= 0 || experts > 1024)
         st = Err(MRUN_ERR_UNSUPPORTED, "permute runs 1..=1024 experts");
+    const size_t need = st.ok() ? mrun_moe_permute_workspace_bytes(pairs, experts) : 0;
+    if (st.ok() && (!workspace || workspace_bytes < need))
+        st = Err(MRUN_ERR_WORKSPACE, "permute needs " + std::to_string(need) + " workspace bytes");
     if (st.ok()) {
         PermuteOut po{};
         po.offsets = offsets, po.order = order, po.inverse = inverse, po.token = token;
-        st = hip_status(launch_permute(ids, pairs, top_k, experts, po, (hipStream_t)stream),
+        st = hip_status(launch_permute(ids, pairs, top_k, experts, (uint32_t *)workspace, po,
+                                       (hipStream_t)stream),
                         "permute");
     }
     return report(st);
 }
 
+int mrun_moe_workspace_routing(const mrun_moe_config *cfg, int32_t tokens, size_t *at) {
+    Status st;
+    if (!cfg || !at) st = Err(MRUN_ERR_INVALID, "cfg and at are required");
+    else if (tokens <= 0) st = Err(MRUN_ERR_INVALID, "tokens must be positive");
+    if (st.ok()) st = check_config(*cfg);
+    if (st.ok()) {
+        const Plan p = make_plan(*cfg, tokens);
+        at[0] = p.ids, at[1] = p.scores, at[2] = p.offsets, at[3] = p.order, at[4] = p.inverse;
+        at[5] = p.token;
+    }
+    return report(st);
+}
+
 size_t mrun_gather_qmm_workspace_bytes(int32_t n, int32_t experts) {
-    if (n <= 0 || experts <= 0) return 0;
+    if (n <= 0 || experts <= 0 || experts > 1024) return 0;
     const size_t max_tiles = (size_t)(n + kGemmTileM - 1) / kGemmTileM + experts;
     return a256(4 * ((size_t)experts + 1)) + a256(4 * (size_t)n) + a256(4 * (size_t)experts) +
-           a256(4) + a256(12 * max_tiles) + a256(4);
+           a256(4) + a256(12 * max_tiles) + a256(4) + a256(4 * permute_counts_words(n, experts));
 }
 
 int mrun_gather_qmm(const mrun_bf16 *x, int32_t x_rows, const mrun_quantized *w,
@@ -663,9 +684,10 @@ int mrun_gather_qmm(const mrun_bf16 *x, int32_t x_rows, const mrun_quantized *w,
         po.active = (uint32_t *)(ws + at), at += a256(4 * (size_t)E);
         po.n_active = (uint32_t *)(ws + at), at += a256(4);
         po.tiles = (uint32_t *)(ws + at), at += a256(12 * max_tiles);
-        po.n_tiles = (uint32_t *)(ws + at);
+        po.n_tiles = (uint32_t *)(ws + at), at += a256(4);
         po.tile_m = kGemmTileM;
-        st = hip_status(launch_permute(indices, n, 1, E, po, s), "gather_qmm permute");
+        uint32_t *counts = (uint32_t *)(ws + at);
+        st = hip_status(launch_permute(indices, n, 1, E, counts, po, s), "gather_qmm permute");
         Routing rt{po.offsets, po.active, po.n_active, po.tiles, po.n_tiles};
         const int per_x = n / x_rows;
         if (st.ok() && n > 16 && w->in % 64 == 0) {

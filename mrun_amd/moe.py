@@ -184,6 +184,24 @@ class SparseMoe:
                                            ws.numel(), _stream(stream)))
         return out
 
+    def routing_of_last_forward(self, tokens: int, workspace: torch.Tensor | None = None):
+        """(ids, scores, offsets, order, inverse, token) that the last forward of `tokens` rows
+        left in its workspace (mrun_moe_workspace_routing). The sorted dispatch (offsets, order,
+        inverse, token) is written by the prefill schedule only."""
+        ws = workspace if workspace is not None else self._ws
+        at = (ctypes.c_size_t * 6)()
+        check(_lib.load().mrun_moe_workspace_routing(ctypes.byref(self.cfg), tokens, at))
+        k, E = self.shape.top_k, self.shape.experts
+        P = tokens * k
+
+        def view(off, n, dtype):
+            nbytes = n * torch.tensor([], dtype=dtype).element_size()
+            return ws[off:off + nbytes].view(dtype)
+
+        return (view(at[0], P, torch.int32), view(at[1], P, torch.bfloat16),
+                view(at[2], E + 1, torch.int32), view(at[3], P, torch.int32),
+                view(at[4], P, torch.int32), view(at[5], P, torch.int32))
+
     def router_forward(self, x: torch.Tensor, stream=None):
         """(logits, gates, ids, scores) of the router (moe.rs:151-159)."""
         T, E, k = x.shape[0], self.shape.experts, self.shape.top_k
@@ -312,8 +330,11 @@ def permute(ids: torch.Tensor, top_k: int, experts: int, stream=None):
     order = torch.empty(P, dtype=torch.int32, device=dev)
     inverse = torch.empty(P, dtype=torch.int32, device=dev)
     token = torch.empty(P, dtype=torch.int32, device=dev)
-    check(_lib.load().mrun_moe_permute(_ptr(ids), P, top_k, experts, _ptr(offsets), _ptr(order),
-                                       _ptr(inverse), _ptr(token), None, 0, _stream(stream)))
+    l = _lib.load()
+    need = int(l.mrun_moe_permute_workspace_bytes(P, experts))
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+    check(l.mrun_moe_permute(_ptr(ids), P, top_k, experts, _ptr(offsets), _ptr(order),
+                             _ptr(inverse), _ptr(token), _ptr(ws), ws.numel(), _stream(stream)))
     return offsets, order, inverse, token
 
 

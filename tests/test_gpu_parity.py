@@ -578,3 +578,269 @@ def test_decode_boundary_t17(q_host, q_dev):
     b = M.bf16_bits(q_dev.forward(M.bf16_tensor(x17[:16])))
     torch.cuda.synchronize()
     assert_close(b, a[:16], what="T=16 decode vs T=17 prefill rows")
+
+
+# ---------------------------------------------------------------------------------------------
+# the sorted dispatch the forward itself uses (moe.rs:65-75), read back from its workspace
+
+def _forward_routing(dev, x, ws):
+    out = dev.forward(x, workspace=ws)
+    ids, sc, off, order, inverse, token = dev.routing_of_last_forward(x.shape[0], ws)
+    torch.cuda.synchronize()
+    return (M.bf16_bits(out), M.u32_array(ids), M.bf16_bits(sc), M.u32_array(off),
+            M.u32_array(order), M.u32_array(inverse), M.u32_array(token))
+
+
+def check_forward_permutation(hb, dev, x_np, label, check_rows=None):
+    """The forward's order / inverse / token are the oracle's stable argsort of the forward's own
+    ids, bit for bit; two forwards leave identical routing and outputs; the ids equal the router
+    op's. Then the block output against the oracle (on check_rows)."""
+    T, k, E = x_np.shape[0], hb.shape.top_k, hb.shape.experts
+    x = M.bf16_tensor(x_np)
+    ws = dev.workspace(T)
+    a = _forward_routing(dev, x, ws)
+    ws2 = torch.empty_like(ws).fill_(0x5A)  # another workspace, different stale contents
+    b = _forward_routing(dev, x, ws2)
+    for name, u, v in zip(("out", "ids", "scores", "offsets", "order", "inverse", "token"), a, b):
+        assert np.array_equal(u, v), f"{label}: {name} differs between two forwards"
+    out, ids, _, off, order, inverse, token = a
+    r_order, r_inverse, r_token, r_counts = O.permute(ids, k, E)
+    assert np.array_equal(order, r_order), f"{label}: order is not the stable argsort"
+    assert np.array_equal(inverse, r_inverse), f"{label}: inverse"
+    assert np.array_equal(token, r_token), f"{label}: token"
+    assert off[0] == 0 and np.array_equal(np.diff(off.astype(np.int64)), r_counts), label
+    _, _, rids, _ = dev.router_forward(x)
+    assert np.array_equal(M.u32_array(rids).ravel(), ids), f"{label}: forward ids differ from the router's"
+    rows = np.arange(T) if check_rows is None else np.asarray(check_rows)
+    ref = O.moe_forward(hb, x_np[rows], forced_ids=ids.reshape(T, k)[rows])
+    s = assert_close(out[rows], ref, what=label)
+    _log(f"{label}: permutation bit-exact ({T * k} pairs), {s}")
+
+
+@pytest.mark.parametrize("T", [17, 300])
+def test_forward_permutation_q(q_host, q_dev, T):
+    x_np = synth.make_x(Q, T, config=synth.CFG_PREFILL_ZIPF, layer=40 + T)
+    check_forward_permutation(q_host, q_dev, x_np, f"Q forward permutation T={T}")
+
+
+def test_forward_permutation_zipf_2048():
+    hb = _zipf_host()
+    dev = M.SparseMoe(hb)
+    x_np = synth.make_x(Q, 2048, config=synth.CFG_PREFILL_ZIPF, layer=7)
+    rows = np.sort(np.random.default_rng(7).choice(2048, 96, replace=False))
+    check_forward_permutation(hb, dev, x_np, "Q Zipf forward permutation T=2048", rows)
+
+
+def test_forward_permutation_8bit_small(q8_blocks):
+    """8-bit experts take the prefill schedule at every size: 24 pairs, the permutation anyway."""
+    hb, dev = q8_blocks["experts8"]
+    x_np = synth.make_x(Q8, 3, config=synth.CFG_DECODE, layer=41)
+    check_forward_permutation(hb, dev, x_np, "8-bit experts forward permutation T=3")
+
+
+def test_block_coder_prefill_8192():
+    """configs[4] prefill, T = 8192 (65,536 pairs): the forward's permutation bit-exact against the
+    stable argsort, and 48 sampled rows of the block output against the oracle (rows are
+    independent of each other, so sampled rows are exact checks)."""
+    hb, dev = _coder_host(), _coder_dev()
+    x_np = synth.make_x(synth.CODER, 8192, config=synth.CFG_CODER, layer=8192)
+    rows = np.sort(np.random.default_rng(8192).choice(8192, 48, replace=False))
+    check_forward_permutation(hb, dev, x_np, "Coder configs[4] T=8192", rows)
+
+
+_ZIPF = {}
+
+
+def _zipf_host():
+    if "host" not in _ZIPF:
+        _ZIPF["host"] = synth.make_block(Q, config=synth.CFG_PREFILL_ZIPF, zipf=True)
+    return _ZIPF["host"]
+
+
+# ---------------------------------------------------------------------------------------------
+# quantized weights without biases: zeros (Quantized::new, nuvec.rs:609-626)
+
+def _without_biases(hb, routed=True, shared=True):
+    """The block with its quantized experts' biases dropped. Their scales get seeded random signs,
+    so that the dequantized weights q*s keep mean zero and the outputs their usual magnitude
+    (with q in 0..15 and positive scales every weight would be positive)."""
+    import copy
+    nb = copy.copy(hb)
+    rng = np.random.default_rng(609)
+
+    def strip(q):
+        sign = rng.integers(0, 2, q.scales.shape, dtype=np.uint16) << np.uint16(15)
+        return synth.QTensor(q.codes, q.scales ^ sign, None, q.experts, q.out, q.in_, q.group,
+                             q.bits)
+
+    if routed:
+        nb.gate_proj, nb.up_proj, nb.down_proj = map(strip, (hb.gate_proj, hb.up_proj, hb.down_proj))
+    if shared and hb.shape.shared:
+        nb.sh_gate_proj, nb.sh_up_proj, nb.sh_down_proj = map(
+            strip, (hb.sh_gate_proj, hb.sh_up_proj, hb.sh_down_proj))
+    return nb
+
+
+@pytest.fixture(scope="module")
+def nobias_blocks(q_host):
+    out = {}
+    for name, kw in {"all": {}, "routed": dict(shared=False)}.items():
+        hb = _without_biases(q_host, **kw)
+        out[name] = (hb, M.SparseMoe(hb))
+    return out
+
+
+@pytest.mark.parametrize("kind", ["all", "routed"])
+@pytest.mark.parametrize("T", [1, 4, 16, 17, 300])
+def test_null_biases_match_oracle(nobias_blocks, kind, T):
+    """Q blocks whose quantized experts (and shared expert) carry no biases, at decode (GEMV
+    kernels) and prefill (MFMA GEMM) sizes, against the oracle's zero-bias dequant."""
+    hb, dev = nobias_blocks[kind]
+    assert hb.gate_proj.biases is None
+    x_np = synth.make_x(Q, T, config=synth.CFG_DECODE, layer=600 + T)
+    run_block(hb, dev, x_np, f"no biases ({kind}) T={T}")
+
+
+def test_null_biases_gather_qmm(q_host):
+    """gather_qmm over a weight without biases, GEMV and MFMA sizes."""
+    w = _without_biases(q_host).down_proj
+    dw = M.DeviceQTensor(w)
+    for n in (8, 600):
+        idx = np.random.default_rng(n).integers(0, Q.experts, n).astype(np.uint32)
+        a_np = synth.make_x(synth.Shape(512, 1, 1, 512), n, config=9, layer=n)
+        got = M.bf16_bits(M.gather_qmm(M.bf16_tensor(a_np), dw, M.u32_tensor(idx)))
+        ref = O.gather_qmm(w, a_np, idx)
+        assert_close(got, ref, max_ulp=1, what=f"gather_qmm without biases n={n}")
+
+
+# ---------------------------------------------------------------------------------------------
+# configs[3]: the 40-layer Qwen-shaped stack (weights generated on the device, 18 GB)
+
+N_STACK = 40
+
+
+@pytest.fixture(scope="module")
+def stack40():
+    layers = [M.device_block(Q, synth.CFG_STACK, l) for l in range(N_STACK)]
+    torch.cuda.synchronize()
+    return layers
+
+
+def _host_view(dev, experts=None):
+    """The device block's weights copied to the host for the oracle; with `experts`, only those
+    experts' slices are copied (the others stay zero pages that the oracle never reads)."""
+    def q(dq):
+        E = dq.experts
+        shp = lambda t: t.view(E, dq.out, -1)
+        if experts is None or len(experts) * 4 >= E:
+            c, s_, b = (M.u32_array(shp(dq.codes)), M.bf16_bits(shp(dq.scales)),
+                        M.bf16_bits(shp(dq.biases)))
+        else:
+            c = np.zeros((E, dq.out, dq.in_ * dq.bits // 32), np.uint32)
+            s_ = np.zeros((E, dq.out, dq.in_ // dq.group), np.uint16)
+            b = np.zeros_like(s_)
+            for e in sorted(experts):
+                c[e] = M.u32_array(shp(dq.codes)[e])
+                s_[e] = M.bf16_bits(shp(dq.scales)[e])
+                b[e] = M.bf16_bits(shp(dq.biases)[e])
+        return synth.QTensor(c, s_, b, E, dq.out, dq.in_, dq.group, dq.bits)
+
+    s = dev.shape
+    hb = synth.HostBlock(shape=s, router=M.bf16_bits(dev.router), router_bias=None,
+                         gate_proj=q(dev.gate_proj), up_proj=q(dev.up_proj),
+                         down_proj=q(dev.down_proj))
+    if s.shared:
+        hb.sh_gate_proj, hb.sh_up_proj, hb.sh_down_proj = (
+            q(dev.sh_gate_proj), q(dev.sh_up_proj), q(dev.sh_down_proj))
+        hb.sh_expert_gate = M.bf16_bits(dev.sh_expert_gate)
+    return hb
+
+
+def _stack_op_loop(layers, x_np, rows):
+    """rms_norm, then per layer the block forward and add_rms_norm. Returns the final x and, per
+    layer, the sampled rows of its input x, its block input h, its block output o, and its ids
+    (read from the forward's own workspace)."""
+    T = x_np.shape[0]
+    x = M.bf16_tensor(x_np)
+    h = M.rms_norm(x, None, 1e-6)
+    trace = []
+    for layer in layers:
+        ws = layer.workspace(T)
+        o = layer.forward(h, workspace=ws)
+        ids = M.u32_array(layer.routing_of_last_forward(T, ws)[0]).reshape(T, -1)[rows].copy()
+        trace.append((M.bf16_bits(x)[rows], M.bf16_bits(h)[rows], M.bf16_bits(o)[rows], ids))
+        x, h = M.add_rms_norm(x, o, None, 1e-6)
+    torch.cuda.synchronize()
+    return M.bf16_bits(x), trace
+
+
+def _stack_bar(got, ref, trace, label):
+    """The block bar for deep layers. L1-relative 1e-3, and each element within max(2e-2, two bf16
+    ulps of the largest term its sum rounds: the routed experts' outputs y_j for that element, the
+    shared expert's output, the result). The synthetic weights s*(q - 8) have mean -s/2, so the
+    residual stream gains a steady direction, and deep in the stack the expert outputs reach
+    |y_j| ~ 10. There one bf16 ulp (0.0625) exceeds 2e-2, and the rounding points inside the
+    block (y_j, y_j * score, the sum over k, the shared add) each move by up to an ulp of their
+    own magnitude under another f32 accumulation order."""
+    T, D = got.shape
+    g, r = synth.bf16_to_f32(got).astype(np.float64), synth.bf16_to_f32(ref).astype(np.float64)
+    terms = np.abs(synth.bf16_to_f32(trace["y"])).reshape(T, -1, D).max(axis=1)
+    if "shared_y" in trace:
+        terms = np.maximum(terms, np.abs(synth.bf16_to_f32(trace["shared_y"])))
+    mag = np.maximum(np.maximum(np.abs(g), np.abs(r)), terms)
+    bound = np.maximum(2e-2, 2 * bf16_ulp(mag))
+    s = stats(got, ref)
+    assert np.all(np.abs(g - r) <= bound), f"{label}: {s}"
+    assert s["l1_rel"] <= 1e-3, f"{label}: {s}"
+    return s
+
+
+def _check_stack_layers(layers, trace, final, label):
+    """Each layer on the GPU's own input for that layer: the norm within one ulp of the oracle's,
+    the block output within the block bar of the oracle's on the GPU's h and ids (each validated
+    as a top-k within ties), and the residual add bit-exact. A 40-layer chain compounds one-ulp
+    roundings (a residual value one ulp off changes the next norm and so the next routing), so
+    the per-layer check is the bar."""
+    worst = None
+    for l, layer in enumerate(layers):
+        x_l, h_l, o_l, ids = trace[l]
+        assert ulp_distance(h_l, O.rms_norm(x_l, None, 1e-6)).max() <= 1, f"{label} layer {l} norm"
+        hb = _host_view(layer, set(np.unique(ids).tolist()))
+        ref, tr = O.moe_forward(hb, h_l, forced_ids=ids, trace=True)
+        if not layer.shared:
+            tr.pop("shared_y")
+        s = _stack_bar(o_l, ref, tr, f"{label} layer {l}")
+        nxt = trace[l + 1][0] if l + 1 < len(layers) else final
+        assert np.array_equal(nxt, O.bf16_from_f32(synth.bf16_to_f32(x_l) + synth.bf16_to_f32(o_l))), \
+            f"{label} layer {l} residual"
+        worst = s if worst is None or s["l1_rel"] > worst["l1_rel"] else worst
+        del hb
+    return worst
+
+
+def test_stack40_decode_t1(stack40):
+    """configs[3] at T = 1: the stack entry point (norm fused into each router launch, residual
+    into the last launch) equals the loop of single ops bit for bit, and every one of the 40 layers
+    matches the oracle on the GPU's input for that layer."""
+    x_np = synth.make_x(Q, 1, config=synth.CFG_STACK, layer=1)
+    st = M.MoeStack(stack40, None, 1e-6)
+    got = M.bf16_bits(st.forward_(M.bf16_tensor(x_np)))
+    loop, trace = _stack_op_loop(stack40, x_np, np.arange(1))
+    assert np.array_equal(got, loop), "stack entry point differs from the op loop"
+    worst = _check_stack_layers(stack40, trace, loop, "stack40 T=1")
+    _log(f"stack of {N_STACK}, T=1: every layer within the bar; worst layer {worst}")
+
+
+def test_stack40_prefill_t4096(stack40):
+    """configs[3] at T = 4096: the stack entry point equals the op loop bit for bit; 32 sampled
+    rows checked layer by layer against the oracle (rows are independent of each other, so
+    sampled rows are exact checks)."""
+    T = 4096
+    x_np = synth.make_x(Q, T, config=synth.CFG_STACK, layer=T)
+    st = M.MoeStack(stack40, None, 1e-6)
+    got = M.bf16_bits(st.forward_(M.bf16_tensor(x_np)))
+    rows = np.sort(np.random.default_rng(4096).choice(T, 32, replace=False))
+    loop, trace = _stack_op_loop(stack40, x_np, rows)
+    assert np.array_equal(got, loop), "stack entry point differs from the op loop"
+    worst = _check_stack_layers(stack40, trace, loop[rows], "stack40 T=4096")
+    _log(f"stack of {N_STACK}, T=4096, 32 rows: every layer within the bar; worst layer {worst}")
