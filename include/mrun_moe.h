@@ -101,6 +101,18 @@ int mrun_moe_forward(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t tok
                      mrun_bf16 *out, void *workspace, size_t workspace_bytes,
                      mrun_stream_t stream);
 
+/* mrun_moe_forward for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). It has no counterpart in the reference.
+ * The workspace is a fixed scratch array inside the library, one per GPU, held until the process
+ * ends: mrun_moe_forward_noalloc_max_bytes() bytes (32 MiB: every decode batch, and prefill
+ * chunks whose mrun_moe_workspace_bytes fits, e.g. a few hundred tokens of the Qwen3.6-like
+ * block). A batch that needs more returns MRUN_ERR_WORKSPACE. The call allocates nothing; the
+ * caller still passes x and out. Every call on one GPU shares that GPU's array, so calls that
+ * overlap in time on one GPU (two streams, two threads) race: serialise them. */
+int mrun_moe_forward_noalloc(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t tokens,
+                             mrun_bf16 *out, mrun_stream_t stream);
+size_t mrun_moe_forward_noalloc_max_bytes(void);
+
 /* mrun_moe_forward with benchmark instrumentation; it has no counterpart in the reference and is
  * for profilers and benchmarks that time each stage on the device. events are hipEvent_t handles
  * created by the caller: events[0] is recorded on the stream before the first launch and

@@ -76,6 +76,10 @@ SIGNATURES = {
         c_int32,
         [POINTER(SparseMoe), c_void_p, c_int32, c_void_p, c_void_p, c_size_t, c_void_p],
     ),
+    "mrun_moe_forward_noalloc": (
+        c_int32, [POINTER(SparseMoe), c_void_p, c_int32, c_void_p, c_void_p],
+    ),
+    "mrun_moe_forward_noalloc_max_bytes": (c_size_t, []),
     "mrun_moe_forward_profiled": (
         c_int32,
         [POINTER(SparseMoe), c_void_p, c_int32, c_void_p, c_void_p, c_size_t, c_void_p,

@@ -13,6 +13,7 @@
 
 #include <cstdint>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "kernels.hpp"
@@ -527,6 +528,69 @@ int mrun_moe_forward(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t tok
     if (st.ok() && x == out) st = Err(MRUN_ERR_INVALID, "out must not alias x");
     if (st.ok())
         st = models::sparse_moe_forward(*moe, x, tokens, out, (char *)workspace, workspace_bytes,
+                                        (hipStream_t)stream);
+    return report(st);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------------------------
+// The forward that allocates nothing: its workspace is a file-scope device array.
+
+namespace mrun {
+
+constexpr size_t kScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// `scratch` names a host-side stand-in in host code; its device address (one per GPU, each GPU
+// holding its own copy) comes from hipGetSymbolAddress, once per device, kept here.
+constexpr int kMaxDevices = 64;
+static void *g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+static Status scratch_of_current_device(void **ptr) {
+    int dev = -1;
+    TRY_HIP(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices)
+        return Err(MRUN_ERR_UNSUPPORTED, "device index " + std::to_string(dev) + " out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        TRY_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        if (!p) return Err(MRUN_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return Ok();
+}
+
+}  // namespace mrun
+
+extern "C" {
+
+size_t mrun_moe_forward_noalloc_max_bytes(void) { return kScratchBytes; }
+
+int mrun_moe_forward_noalloc(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t tokens,
+                             mrun_bf16 *out, mrun_stream_t stream) {
+    Status st = check_block(moe);
+    if (st.ok() && tokens < 0) st = Err(MRUN_ERR_INVALID, "tokens must not be negative");
+    if (st.ok() && tokens == 0) return report(st);  // an empty batch: nothing to do
+    if (st.ok()) st = check_ptr(x, "x");
+    if (st.ok()) st = check_ptr(out, "out");
+    if (st.ok() && x == out) st = Err(MRUN_ERR_INVALID, "out must not alias x");
+    if (st.ok()) {
+        const size_t need = make_plan(moe->cfg, tokens).total;
+        if (need > kScratchBytes)
+            st = Err(MRUN_ERR_WORKSPACE,
+                     "forward_noalloc: " + std::to_string(tokens) + " tokens need " +
+                         std::to_string(need) + " bytes of scratch, above its fixed " +
+                         std::to_string(kScratchBytes) + " bytes (use mrun_moe_forward with a "
+                                                         "workspace)");
+    }
+    void *ws = nullptr;
+    if (st.ok()) st = scratch_of_current_device(&ws);
+    if (st.ok())
+        st = models::sparse_moe_forward(*moe, x, tokens, out, (char *)ws, kScratchBytes,
                                         (hipStream_t)stream);
     return report(st);
 }
