@@ -388,8 +388,8 @@ static Status params(const std::string &path, const json::Value &v, std::optiona
                      std::optional<QParams> &out) {
     if (const json::Value *mode = v.get("mode"); mode && mode->kind == json::Value::Str &&
                                                  mode->str != "affine")
-        return invalid("quantization",
-                       path + ": mode " + mode->str + " is not supported (only affine)");
+        return invalid("quantization", path + ": quantization mode " + mode->str +
+                                           " cannot be loaded; this build reads affine codes");
     std::optional<int> g, b;
     if (const json::Value *x = v.get("group_size"); x && x->is_int()) g = (int)x->num;
     else if (base) g = base->group_size;
@@ -404,10 +404,10 @@ static Status checked(const std::string &path, QParams q) {
     const bool bits = q.bits == 4 || q.bits == 8;
     const bool group = q.group_size == 32 || q.group_size == 64 || q.group_size == 128;
     if (!bits || !group)
-        return invalid("quantization", path + ": " + std::to_string(q.bits) +
-                                           " bits with group size " + std::to_string(q.group_size) +
-                                           " is not supported (affine 4 or 8 bits, groups of 32, "
-                                           "64 or 128)");
+        return invalid("quantization", path + ": affine codes of " + std::to_string(q.bits) +
+                                           " bits in groups of " + std::to_string(q.group_size) +
+                                           " cannot be loaded; accepted: 4- or 8-bit codes, "
+                                           "groups of 32/64/128");
     return Ok();
 }
 
@@ -436,20 +436,21 @@ static Status quantization_from_config(const json::Value &config, Quantization &
 static Status infer(const std::string &path, const Tensor &weight, const Tensor &scales,
                     int in_dims, QParams &out) {
     if (scales.dtype == "U8")
-        return invalid("quantization",
-                       path + ": uint8 scales (mxfp4, nvfp4 or mxfp8) are not supported (only affine)");
+        return invalid("quantization", path + ": U8 scales belong to a microscaling format; "
+                                           "this build reads affine codes with bf16 scales");
     if (weight.shape.empty() || scales.shape.empty())
-        return invalid("quantization", path + ": scalar weight or scales");
+        return invalid("quantization", path + ": weight and scales need at least one dimension");
     const int64_t groups = scales.dim(-1);
     if (in_dims <= 0 || groups <= 0 || in_dims % groups != 0)
-        return invalid("quantization", path + ": " + std::to_string(groups) +
-                                           " scale groups do not divide the input width " +
-                                           std::to_string(in_dims));
+        return invalid("quantization", path + ": an input width of " + std::to_string(in_dims) +
+                                           " is no whole number of " + std::to_string(groups) +
+                                           " groups");
     const int64_t packed = weight.dim(-1) * 32;
     if (packed % in_dims != 0)
-        return invalid("quantization", path + ": " + std::to_string(weight.dim(-1)) +
-                                           " packed words do not hold whole " +
-                                           std::to_string(in_dims) + "-wide rows");
+        return invalid("quantization", path + ": a row of " + std::to_string(weight.dim(-1)) +
+                                           " u32 words packs no whole number of bits per code "
+                                           "for an input width of " +
+                                           std::to_string(in_dims));
     out = QParams{(int)(in_dims / groups), (int)(packed / in_dims)};
     return checked(path, out);
 }
@@ -460,7 +461,8 @@ static Status resolve(const Quantization &q, const std::string &path, const Tens
     auto it = q.overrides.find(path);
     if (it != q.overrides.end()) {
         if (!it->second)
-            return invalid("quantization", path + " is quantized but the config marks it unquantized");
+            return invalid("quantization", path + " has codes and scales on disk, while "
+                                                  "config.json lists it as a plain tensor");
         out = *it->second;
         return Ok();
     }

@@ -69,14 +69,14 @@ static Status check_quantized(const mrun_quantized *q, const std::string &path, 
     const bool bits_ok = q->bits == 4 || q->bits == 8;
     const bool group_ok = q->group_size == 32 || q->group_size == 64 || q->group_size == 128;
     if (!bits_ok || !group_ok)
-        return Err(MRUN_ERR_INVALID, path + ": " + std::to_string(q->bits) +
-                                         " bits with group size " + std::to_string(q->group_size) +
-                                         " is not supported (affine 4 or 8 bits, groups of 32, "
-                                         "64 or 128)");
+        return Err(MRUN_ERR_INVALID, path + ": bits = " + std::to_string(q->bits) +
+                                         ", group_size = " + std::to_string(q->group_size) +
+                                         "; a quantized weight has 4 or 8 bits and groups of "
+                                         "32, 64 or 128 (16 bits: dense bf16)");
     if (q->in % q->group_size != 0)
-        return Err(MRUN_ERR_INVALID, path + ": " + std::to_string(q->in / q->group_size) +
-                                         " scale groups do not divide the input width " +
-                                         std::to_string(q->in));
+        return Err(MRUN_ERR_INVALID, path + ": input width " + std::to_string(q->in) +
+                                         " is not a multiple of group_size " +
+                                         std::to_string(q->group_size));
     if (q->in % (128 / q->bits) != 0)
         return Err(MRUN_ERR_UNSUPPORTED, path + ": input width " + std::to_string(q->in) +
                                              " must be a multiple of " +

@@ -110,8 +110,8 @@ def test_valid_blocks_pass():
 
 
 @pytest.mark.parametrize("over,code,text", [
-    ({"switch_gate_proj": q(256, 512, 2048, group=16)}, _lib.MRUN_ERR_INVALID, "group size 16"),
-    ({"switch_gate_proj": q(256, 512, 2048, bits=3)}, _lib.MRUN_ERR_INVALID, "3 bits"),
+    ({"switch_gate_proj": q(256, 512, 2048, group=16)}, _lib.MRUN_ERR_INVALID, "group_size = 16"),
+    ({"switch_gate_proj": q(256, 512, 2048, bits=3)}, _lib.MRUN_ERR_INVALID, "bits = 3"),
     ({"switch_gate_proj": q(256, 512, 2048, bits=8)}, _lib.MRUN_ERR_UNSUPPORTED,
      "gate_proj and up_proj must share"),
     ({"switch_down_proj": q(256, 512, 2048)}, _lib.MRUN_ERR_INVALID, "down_proj: shape"),
@@ -121,7 +121,7 @@ def test_valid_blocks_pass():
     ({"gate": Linear(None, q(1, 128, 2048, bits=8), None, 256, 2048)}, _lib.MRUN_ERR_INVALID,
      "gate: shape [1, 128, 2048], expected [1, 256, 2048]"),
     ({"shared_expert_gate": Linear(None, q(1, 1, 2048, bits=8, group=48), None, 1, 2048)},
-     _lib.MRUN_ERR_INVALID, "group size 48"),
+     _lib.MRUN_ERR_INVALID, "group_size = 48"),
 ])
 def test_invalid_blocks_are_refused(over, code, text):
     rc, msg = status(block(**over))
@@ -161,7 +161,7 @@ def test_op_argument_errors():
     assert rc == _lib.MRUN_ERR_INVALID
     w = q(4, 64, 100)
     rc = lib.mrun_gather_qmm(FAKE, 2, ctypes.byref(w), FAKE, 4, 0, FAKE, FAKE, 1 << 20, None)
-    assert rc == _lib.MRUN_ERR_INVALID and "scale groups" in lib.mrun_last_error().decode()
+    assert rc == _lib.MRUN_ERR_INVALID and "not a multiple of group_size" in lib.mrun_last_error().decode()
 
 
 def test_empty_batches_are_no_ops():
