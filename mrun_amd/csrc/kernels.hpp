@@ -62,6 +62,8 @@ struct PermuteOut {
     uint32_t *tiles;     // [3 * max_tiles] or null
     uint32_t *n_tiles;   // [1] or null
     int tile_m;          // rows per tile
+    uint32_t *tile_rows; // [max tiles][tile_m] token (pair / k) of each tile row, or null; rows
+                         // past a partial tile's end repeat its last row
 };
 hipError_t launch_topk(const bf16_t *logits, int T, int E, int k, bool norm, bf16_t *gates,
                        uint32_t *ids, bf16_t *scores, hipStream_t stream);
@@ -181,6 +183,47 @@ bool qgemm_supported(const GemmJob &job);
 constexpr int kGemmTileM = 64;  // rows per routed tile
 
 constexpr int kGemmTileN = 64;
+
+// The prefill forward's grouped expert GEMM (moe_gemm.hip): 4-bit group-64 weights (biases may be
+// null), K % 512 == 0, N a multiple of 128 (glu) or 256. A is packed (launch_apack) with its X
+// splits AX [rows][3][ax_e] (ax_e = K / 64, or 2 K / 64 for two half-group sums per group).
+// Routed tiles come from routing.tiles (64 rows); their A rows from tile_rows [tile][64] (token
+// of each tile row, the tile's last row repeated past its rows) or, without tile_rows, the sorted
+// positions themselves. glu: out = packed R(silu(R(A.w0)) * R(A.w1)) and OX [rows][3][2 N / 64]
+// the X splits of each output row's half groups; else out = R(A.w0). The shared product (sh)
+// has the same K and N and comes first.
+struct MoeGemmJob {
+    const bf16_t *A;
+    int lda;
+    const bf16_t *AX;
+    int ax_e;
+    const uint32_t *tile_rows;
+    int K, N, glu;
+    QW w0, w1;
+    Routing routing;
+    int has_routing, max_tiles;
+    int M;
+    bf16_t *out;
+    int ldo;
+    bf16_t *OX;
+    struct {
+        const bf16_t *A;
+        int lda;
+        const bf16_t *AX;
+        int ax_e;
+        int M;
+        QW w0, w1;
+        bf16_t *out;
+        int ldo;
+        bf16_t *OX;
+    } sh;
+    int has_shared;
+};
+bool moe_gemm_supported(const MoeGemmJob &j);
+hipError_t launch_moe_gemm(const MoeGemmJob &j, hipStream_t stream);
+// x [rows][K] (row stride lda) -> packed rows (stride ldp) and X splits [rows][3][K / 64]
+hipError_t launch_apack(const bf16_t *x, int lda, int rows, int K, bf16_t *xp, int ldp,
+                        bf16_t *xs, hipStream_t stream);
 
 // Dense bf16 Linear for more than 16 rows on the MFMAs (dense.hip): out0 = R(A W0^T) then
 // R(. + bias0), and optionally out1 from W1 in the same launch (the shared expert's gate beside the

@@ -167,6 +167,7 @@ struct Plan {
     size_t logits, ids, scores, offsets, order, inverse, token, active, n_active, tiles, n_tiles;
     size_t counts;
     int n_counts;
+    size_t xp, xs, act_x, sh_act_x, tile_rows;  // the packed operands of the prefill GEMMs
     size_t act, y, sh_logit, sh_act, sh_y, total;
     int max_tiles;
 };
@@ -205,6 +206,15 @@ static Plan make_plan(const mrun_moe_config &c, int T) {
         p.sh_logit = take(2 * (size_t)T);
         p.sh_act = take(2 * (size_t)T * S);
         p.sh_y = take(2 * (size_t)T * D);
+    }
+    // prefill GEMM operands (moe_gemm.hip): packed x and its group-sum splits, the half-group
+    // splits of act (and of the shared expert's act), the token rows of each routed tile
+    if (T > 16) {
+        p.xp = take(2 * (size_t)T * D);
+        p.xs = take(2 * 3 * (size_t)T * (D / 64));
+        p.act_x = take(2 * 3 * P * (2 * (I / 64)));
+        if (S > 0) p.sh_act_x = take(2 * 3 * (size_t)T * (2 * (S / 64)));
+        p.tile_rows = take(4 * (size_t)p.max_tiles * kGemmTileM);
     }
     p.total = at;
     return p;
@@ -425,9 +435,61 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
     PermuteOut pt = po;
     pt.tiles = (uint32_t *)at(p.tiles);
     pt.n_tiles = (uint32_t *)at(p.n_tiles);
+    const bool packs = mfma && T > 16 && D % 512 == 0 && I % 512 == 0;
+    if (packs) pt.tile_rows = (uint32_t *)at(p.tile_rows);
     TRY_HIP(launch_route_scatter(ids, counts, T, k, E, pt, s), "scatter");
+    if (packs)
+        TRY_HIP(launch_apack(x, D, T, D, (bf16_t *)at(p.xp), D, (bf16_t *)at(p.xs), s), "pack x");
     st.mark(s);
-    if (mfma) {
+    // the grouped GEMM of moe_gemm.hip: 4-bit group-64 experts, K a multiple of 512, the shared
+    // expert in the same launches when its width equals the routed one
+    MoeGemmJob mg{}, md{};
+    bool new_path = false, fuse_new = false;
+    if (mfma && T > 16) {
+        mg.A = (const bf16_t *)at(p.xp), mg.lda = D, mg.AX = (const bf16_t *)at(p.xs);
+        mg.ax_e = D / 64, mg.tile_rows = (const uint32_t *)at(p.tile_rows);
+        mg.K = D, mg.N = I, mg.glu = 1;
+        mg.w0 = qw_of(m.switch_gate_proj), mg.w1 = qw_of(m.switch_up_proj);
+        mg.routing = rt, mg.has_routing = 1, mg.max_tiles = p.max_tiles;
+        mg.out = act, mg.ldo = I, mg.OX = (bf16_t *)at(p.act_x);
+        md.A = act, md.lda = I, md.AX = (const bf16_t *)at(p.act_x), md.ax_e = 2 * (I / 64);
+        md.K = I, md.N = D, md.glu = 0, md.w0 = qw_of(m.switch_down_proj);
+        md.routing = rt, md.has_routing = 1, md.max_tiles = p.max_tiles, md.out = y, md.ldo = D;
+        new_path = moe_gemm_supported(mg) && moe_gemm_supported(md);
+        if (new_path && S == I && !m.shared_gate_proj.weight && !m.shared_up_proj.weight &&
+            !m.shared_down_proj.weight) {
+            MoeGemmJob tg = mg, td = md;
+            tg.sh = {mg.A, D, mg.AX, D / 64, T, qw_of(m.shared_gate_proj.q),
+                     qw_of(m.shared_up_proj.q), sh_act, S, (bf16_t *)at(p.sh_act_x)};
+            tg.has_shared = 1;
+            td.sh = {sh_act, S, (const bf16_t *)at(p.sh_act_x), 2 * (S / 64), T,
+                     qw_of(m.shared_down_proj.q), QW{}, sh_y, D, nullptr};
+            td.has_shared = 1;
+            if (moe_gemm_supported(tg) && moe_gemm_supported(td)) mg = tg, md = td, fuse_new = true;
+        }
+    }
+    if (new_path) {
+        TRY_HIP(launch_moe_gemm(mg, s), "gate/up (moe gemm)");
+        st.mark(s);
+        TRY_HIP(launch_moe_gemm(md, s), "down (moe gemm)");
+        st.mark(s);
+        if (S && !fuse_new) {  // a shared expert of another width or format: the generic GEMMs
+            GemmJob sg{}, sd{};
+            sg.A = x, sg.lda = D, sg.a_div = 1, sg.M = T, sg.N = S, sg.K = D;
+            sg.w0 = qw_of(as_quantized(m.shared_gate_proj));
+            sg.w1 = qw_of(as_quantized(m.shared_up_proj));
+            sg.out = sh_act, sg.ldo = S, sg.glu = 1;
+            sd.A = sh_act, sd.lda = S, sd.a_div = 1, sd.M = T, sd.N = D, sd.K = S;
+            sd.w0 = qw_of(as_quantized(m.shared_down_proj)), sd.out = sh_y, sd.ldo = D;
+            TRY_HIP(launch_gemm(sg, s), "shared gate/up (mfma)");
+            st.mark(s);
+            TRY_HIP(launch_gemm(sd, s), "shared down (mfma)");
+            st.mark(s);
+        } else {
+            st.mark(s);
+            st.mark(s);
+        }
+    } else if (mfma) {
         GemmJob g{};
         g.A = x, g.lda = D, g.a_map = po.order, g.a_div = k, g.N = I, g.K = D;
         g.w0 = qw_of(m.switch_gate_proj), g.w1 = qw_of(m.switch_up_proj);

@@ -1,0 +1,627 @@
+// The prefill forward's expert products on the matrix cores (gfx950 v_mfma_f32_32x32x16_bf16):
+// SwitchGlu's gate/up with SwiGLU, and down (moe.rs:79-83; gather_qmm with sorted indices,
+// nuvec.rs:670-686), with the shared expert's products as extra tiles of the same launches.
+//
+// The affine dequant is folded around the MFMA. A code q sits in the low mantissa bits of bf16
+// 128.0 (0x4300 | q == 128 + q exactly), so one and-or turns a code word into the B operand; the
+// MFMA chain over one quant group (64 k) gives P' = sum x (128 + q) in f32, and the group enters
+// the result as  s * P' + (b - 128 s) * X  with X = sum x over the group. No weight is rounded.
+//
+// Operand layout (prepared once per row, outside the K loop):
+//  - A rows are "packed": in each 64-wide group the eight 8-element k blocks are stored in the
+//    order the MFMA fragments read them (block 4h + s at position 2s + h: K sub-step s, lane half
+//    h) and each block is re-paired (x0, x4, x1, x5, x2, x6, x3, x7) to match the code expansion
+//    (dword i of an expanded word holds codes i and i + 4). The GEMM copies A into LDS unchanged.
+//  - X is stored split exactly into three bf16 (hi + mid + lo == X, truncation) per entry:
+//    XS [rows][3][entries]. apack_kernel writes one entry per group of x; the gate/up epilogue
+//    writes two per group of act (each workgroup wave covers half of a 64-column group), and the
+//    bias term sums both.
+//  - The bias term  sum_g X_g (b_g - 128 s_g)  is a small MFMA product per tile: K entries of
+//    X splits against b (lane half 0) and -128 s (lane half 1; exact), 3 MFMAs per 8 entries.
+//
+// Schedule: persistent workgroups (two per CU, 4 waves) walk a list of items (64-row tile x
+// column block of 256 B rows; under glu 128 gate + 128 up rows). The list is cut into eight
+// contiguous segments, one per XCD (the hardware deals workgroup L to XCD L % 8), so the column
+// blocks of a row tile run side by side on one XCD and share its L2 for the A rows. The K steps
+// of consecutive items form one stream: A and codes go from global memory straight into LDS
+// (global_load_lds, no VGPRs, no VALU), four K steps in flight, the next item's first steps
+// loading during this item's epilogue. Each wave owns 64 rows x 64 B rows (2 x 2 fragments) and
+// per K step issues 16 MFMAs, expands 8 code words and applies the group scale with 64 FMAs.
+// LDS reads are inline ds_read with explicit lgkmcnt waits, and the DMA waits are explicit
+// vmcnt counts, so the compiler inserts no wait of its own on the LDS that the DMA fills.
+#include <type_traits>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace mrun {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 mg_bf16x8;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float mg_f32x16;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+namespace mg {
+constexpr int BM = 64, BK = 64, BNR = 256, NS = 4, NT = 256;
+constexpr int A_BYTES = BM * BK * 2;           // one K step of A: 64 rows x 128 B
+constexpr int C_BYTES = BNR * BK / 2;          // one K step of codes: 256 B rows x 32 B
+constexpr int STAGE = A_BYTES + C_BYTES;
+constexpr int S_BYTES = BNR * 16;              // scales of 8 groups per B row
+constexpr int R_BYTES = BM * 4;                // A rows (tokens) of a routed tile
+constexpr int X_BYTES = BM * 3 * 16;           // bias term: X splits of 8 entries per row
+constexpr int B_BYTES = BNR * 16;              // bias term: biases of 8 groups per B row
+constexpr int OFF_S = NS * STAGE, OFF_R = OFF_S + 2 * S_BYTES, OFF_X = OFF_R + 3 * R_BYTES;
+constexpr int OFF_B = OFF_X + X_BYTES;
+constexpr int LDS_BYTES = OFF_B + B_BYTES;     // 81,664: two workgroups per CU
+}  // namespace mg
+
+__device__ __forceinline__ uint32_t lds_offset(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
+}
+template <int OFF>
+__device__ __forceinline__ u32x4 ds_read16(uint32_t a) {
+    u32x4 v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+    return v;
+}
+__device__ __forceinline__ uint32_t ds_read4(uint32_t a) {
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(a));
+    return v;
+}
+__device__ __forceinline__ uint32_t ds_read2(uint32_t a) {
+    uint32_t v;
+    asm volatile("ds_read_u16 %0, %1" : "=v"(v) : "v"(a));
+    return v;
+}
+// 16 (or 4) bytes per lane from global memory into LDS at lds + 16 * lane (4 * lane): the LDS
+// address must be the same for the whole wave.
+__device__ __forceinline__ void dma16(const void *g, char *lds) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void_t *)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void *g, char *lds) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void_t *)lds, 4, 0, 0);
+}
+// Wait until at most N of this wave's global loads are outstanding, then a workgroup barrier.
+template <int N>
+__device__ __forceinline__ void vm_wait_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"i"(N) : "memory");
+}
+
+__device__ __forceinline__ u32x4 mg_expand(uint32_t w, uint32_t cm, uint32_t cx) {
+    u32x4 r;
+    r.x = (w & cm) | cx;
+    r.y = ((w >> 4) & cm) | cx;
+    r.z = ((w >> 8) & cm) | cx;
+    r.w = ((w >> 12) & cm) | cx;
+    return r;
+}
+
+// -128 s for a pair of bf16 scales (exact: a power-of-two scaling)
+__device__ __forceinline__ uint32_t mg_neg128(uint32_t w) {
+    const uint32_t lo = __float_as_uint(-128.f * bf_lo(w)) >> 16;
+    const uint32_t hi = __float_as_uint(-128.f * bf_hi(w)) & 0xFFFF0000u;
+    return lo | hi;
+}
+
+// X split exactly into three bf16: hi + mid + lo == x (truncations of f32)
+__device__ __forceinline__ void split3(float x, uint32_t &hi, uint32_t &mid, uint32_t &lo) {
+    const float h = __uint_as_float(__float_as_uint(x) & 0xFFFF0000u);
+    const float r1 = x - h;
+    const float m = __uint_as_float(__float_as_uint(r1) & 0xFFFF0000u);
+    hi = __float_as_uint(h) >> 16;
+    mid = __float_as_uint(m) >> 16;
+    lo = __float_as_uint(r1 - m) >> 16;
+}
+
+// ---------------------------------------------------------------------------------------------
+// A packing: x [rows][K] (row stride lda) -> packed rows [rows][K] (stride ldp) and the X splits
+// [rows][3][K / 64]. One thread per 8-element block; the 8 threads of a group are adjacent lanes.
+
+__global__ __launch_bounds__(256) void apack_kernel(const bf16_t *__restrict__ x, int lda, int rows,
+                                                    int K, bf16_t *__restrict__ xp, int ldp,
+                                                    bf16_t *__restrict__ xs) {
+    const int nb = K / 8;
+    const long long b = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (b >= (long long)rows * nb) return;  // whole groups only: rows * nb is a multiple of 8
+    const int row = (int)(b / nb), blk = (int)(b % nb), g = blk >> 3, w = blk & 7;
+    const uint4 v = *(const uint4 *)(x + (size_t)row * lda + (size_t)blk * 8);
+    const uint4 p = make_uint4(__builtin_amdgcn_perm(v.z, v.x, 0x05040100u),
+                               __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+                               __builtin_amdgcn_perm(v.w, v.y, 0x05040100u),
+                               __builtin_amdgcn_perm(v.w, v.y, 0x07060302u));
+    const int pos = 2 * (w & 3) + (w >> 2);
+    *(uint4 *)(xp + (size_t)row * ldp + g * 64 + pos * 8) = p;
+    float s = bf_lo(v.x) + bf_hi(v.x);
+    s += bf_lo(v.y) + bf_hi(v.y);
+    s += bf_lo(v.z) + bf_hi(v.z);
+    s += bf_lo(v.w) + bf_hi(v.w);
+    s = group_sum<8>(s);
+    if (w == 0) {
+        uint32_t hi, mid, lo;
+        split3(s, hi, mid, lo);
+        const int G = K / 64;
+        bf16_t *d = xs + (size_t)row * 3 * G + g;
+        d[0] = (bf16_t)hi;
+        d[G] = (bf16_t)mid;
+        d[2 * G] = (bf16_t)lo;
+    }
+}
+
+hipError_t launch_apack(const bf16_t *x, int lda, int rows, int K, bf16_t *xp, int ldp,
+                        bf16_t *xs, hipStream_t stream) {
+    const long long n = (long long)rows * (K / 8);
+    if (n == 0) return hipSuccess;
+    apack_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(x, lda, rows, K, xp, ldp, xs);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------
+// the grouped GEMM
+
+// A value the whole wave holds, moved to a scalar register: integer divisions by runtime values
+// run on the VALU, and without this the compiler would treat their results (and the loads and
+// branches that depend on them) as per-lane.
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+// A pointer the whole wave holds, in scalar registers (so that a per-lane choice between two such
+// pointers is a select of values, not a per-lane load of the kernel argument holding them).
+template <class T>
+__device__ __forceinline__ const T *unip(const T *p) {
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const T *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+// A routed tile's record (expert, first row, rows) through the scalar cache. The tile list is
+// written by an earlier launch and only read by this one; a plain load would go through the
+// vector memory counter, whose waits would also wait for the global-to-LDS copies in flight.
+__device__ __forceinline__ void tile_record(const uint32_t *t3, int &e, int &row0, int &mrows) {
+    uint64_t ab;
+    uint32_t c;
+    asm volatile("s_load_dwordx2 %0, %2, 0x0\n\ts_load_dword %1, %2, 0x8\n\ts_waitcnt lgkmcnt(0)"
+                 : "=s"(ab), "=s"(c)
+                 : "s"(t3)
+                 : "memory");
+    e = (int)(uint32_t)ab, row0 = (int)(uint32_t)(ab >> 32), mrows = (int)c;
+}
+
+template <bool GLU>
+__global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
+    using namespace mg;
+    __shared__ __align__(16) char smem[LDS_BYTES];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int fr = lane & 31, fh = lane >> 5;
+    const uint32_t lds0 = lds_offset(smem);
+    char *const rowbuf = smem + OFF_R;
+
+    constexpr int NCOLS = GLU ? 128 : 256;
+    const int NB = j.N / NCOLS;
+    const int s_tiles = j.has_shared ? (j.sh.M + BM - 1) / BM : 0;
+    const int r_tiles =
+        j.has_routing ? min((int)*j.routing.n_tiles, j.max_tiles) : (j.M + BM - 1) / BM;
+    const int total = (s_tiles + r_tiles) * NB;
+    const int G8 = (int)(gridDim.x >> 3), xcd = (int)(blockIdx.x & 7), slot = (int)(blockIdx.x >> 3);
+    const int seg_lo = (int)((long long)total * xcd / 8);
+    const int seg_hi = (int)((long long)total * (xcd + 1) / 8);
+    const int n_items = uni(seg_hi - seg_lo > slot ? (seg_hi - seg_lo - slot + G8 - 1) / G8 : 0);
+    if (n_items == 0) return;
+    const int K = j.K, nks = K / BK, G = K / 64;
+    const int total_steps = n_items * nks;  // a multiple of 8
+
+    // item n of this workgroup: (row tile, column block); shared tiles come first
+    struct Item {
+        int e, row0, mrows, n0, tile;  // tile: routed tile index (rows from the table), or -1
+        bool sh;
+    };
+    auto item_of = [&](int n) __attribute__((always_inline)) {
+        const int i = seg_lo + slot + G8 * n;
+        const int rt = uni(i / NB), cb = i - rt * NB;
+        Item it;
+        it.n0 = cb * NCOLS;
+        if (rt < s_tiles) {
+            it.sh = true, it.e = 0, it.row0 = rt * BM, it.mrows = min(BM, j.sh.M - it.row0);
+            it.tile = -1;
+        } else {
+            it.sh = false;
+            const int r = rt - s_tiles;
+            if (j.has_routing) {
+                tile_record(j.routing.tiles + 3 * (size_t)r, it.e, it.row0, it.mrows);
+                it.tile = j.tile_rows ? r : -1;
+            } else {
+                it.e = 0, it.row0 = r * BM, it.mrows = min(BM, j.M - it.row0), it.tile = -1;
+            }
+        }
+        return it;
+    };
+
+    // ---- load role: A rows ra, ra + 32 (16-byte unit ua), B rows rb, rb + 128 (unit uc), scale
+    // row tid. Units are XOR-swizzled so that the fragment reads of 8 lanes (a 128-byte LDS
+    // cycle) fall on distinct banks: A unit u of row r sits at u ^ (r & 7), code unit u of B row R
+    // at u ^ ((R >> 2) & 1).
+    const int ra = wave * 8 + (lane >> 3);
+    const uint32_t ua16 = 16u * (uint32_t)((lane & 7) ^ (ra & 7));
+    const int rb = tid >> 1;
+    const uint32_t uc16 = 16u * (uint32_t)((tid & 1) ^ ((rb >> 2) & 1));
+    // byte offsets of this lane's DMA sources from the item's (scalar) base pointers
+    const char *a_base = nullptr, *c_base0 = nullptr, *c_base1 = nullptr, *s_base = nullptr;
+    uint32_t la0 = 0, la1 = 0, lc0 = 0, lc1 = 0, ls = 0;
+    int l_item = 0, l_ks = 0;
+
+    // the A row (token) of tile row r of item n
+    auto a_row = [&](const Item &it, int n, int r) __attribute__((always_inline)) -> int {
+        const int rr = min(r, it.mrows - 1);
+        if (it.tile >= 0) return (int)ds_read4(lds0 + OFF_R + (n % 3) * R_BYTES + 4 * rr);
+        return it.row0 + rr;
+    };
+    // copy the token rows of item n's routed tile into its row buffer (wave 0)
+    auto fetch_rows = [&](int n) __attribute__((always_inline)) {
+        if (n >= n_items || wave != 0) return;
+        const Item it = item_of(n);
+        if (it.tile < 0) return;
+        dma4(j.tile_rows + (size_t)it.tile * BM + lane, rowbuf + (n % 3) * R_BYTES);
+    };
+    auto setup_load = [&](int n) __attribute__((always_inline)) {
+        const Item it = item_of(n);
+        int r0 = a_row(it, n, ra), r1 = a_row(it, n, ra + 32);
+        if (it.tile >= 0) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r0), "+v"(r1));
+        const int lda = it.sh ? j.sh.lda : j.lda;
+        a_base = (const char *)(it.sh ? j.sh.A : j.A);
+        la0 = (uint32_t)r0 * (uint32_t)lda * 2u + ua16;
+        la1 = (uint32_t)r1 * (uint32_t)lda * 2u + ua16;
+        c_base0 = (const char *)(it.sh ? j.sh.w0.codes : j.w0.codes);
+        c_base1 = GLU ? (const char *)(it.sh ? j.sh.w1.codes : j.w1.codes) : c_base0;
+        const uint32_t wrow = (uint32_t)it.e * (uint32_t)(it.sh ? j.sh.w0.out : j.w0.out);
+        const uint32_t col0 = (uint32_t)(it.n0 + rb), col1 = GLU ? col0 : col0 + 128u;
+        lc0 = (wrow + col0) * (uint32_t)(K / 2) + uc16;
+        lc1 = (wrow + col1) * (uint32_t)(K / 2) + uc16;
+        const bool up = GLU && tid >= 128;
+        const char *sg = (const char *)unip(it.sh ? j.sh.w0.scales : j.w0.scales);
+        const char *su = GLU ? (const char *)unip(it.sh ? j.sh.w1.scales : j.w1.scales) : sg;
+        s_base = up ? su : sg;
+        ls = (wrow + (uint32_t)(GLU ? it.n0 + (tid & 127) : it.n0 + tid)) * (uint32_t)G * 2u;
+        fetch_rows(n + 1);  // one item ahead
+    };
+    // issue the DMA of global step gl (the load cursor's item and K step) into ring stage ST
+    auto issue = [&](int gl, auto st_c) __attribute__((always_inline)) {
+        constexpr int ST = decltype(st_c)::value;
+        char *sa = smem + ST * STAGE, *sc = sa + A_BYTES;
+        // nks is a multiple of 8 and the stream starts at step 0 of an item, so a chunk of
+        // scales can only start at ring stage 0 and an item can only end at ring stage 3
+        if constexpr (ST == 0)
+            if ((l_ks & 7) == 0)  // the scale chunk of K steps l_ks .. l_ks + 7
+                dma16(s_base + ls + 2 * l_ks, smem + OFF_S + ((gl >> 3) & 1) * S_BYTES + wave * 1024);
+        dma16(a_base + la0 + l_ks * 128, sa + wave * 1024);
+        dma16(a_base + la1 + l_ks * 128, sa + 4096 + wave * 1024);
+        dma16(c_base0 + lc0 + l_ks * 32, sc + wave * 1024);
+        dma16(c_base1 + lc1 + l_ks * 32, sc + 4096 + wave * 1024);
+        ++l_ks;
+        if constexpr (ST == 3)
+            if (l_ks == nks) {
+                l_ks = 0;
+                if (++l_item < n_items) setup_load(l_item);
+            }
+    };
+
+    // ---- compute role: rows mi * 32 + fr, B rows bro[ni] + fr
+    uint32_t a_off[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+        a_off[s] = lds0 + (uint32_t)(fr * 128 + 16 * ((2 * s + fh) ^ (fr & 7)));
+    const uint32_t c_off = (uint32_t)(fr * 32 + 16 * (fh ^ ((fr >> 2) & 1)));
+    const int bro0 = GLU ? wave * 32 : wave * 64, bro1 = GLU ? 128 + wave * 32 : wave * 64 + 32;
+    const uint32_t c_addr0 = lds0 + (uint32_t)bro0 * 32 + c_off, c_addr1 = lds0 + (uint32_t)bro1 * 32 + c_off;
+    const uint32_t s_addr0 = lds0 + OFF_S + (uint32_t)(bro0 + fr) * 16;
+    const uint32_t s_addr1 = lds0 + OFF_S + (uint32_t)(bro1 + fr) * 16;
+    uint32_t cm = 0x000F000Fu, cx = 0x43004300u;  // in VGPRs, so that and-or fuses
+    asm volatile("" : "+v"(cm), "+v"(cx));
+
+    mg_f32x16 acc[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[mi][ni][i] = 0.f;
+
+    // ---- prologue: rows of item 0, then the first NS - 1 stages
+    fetch_rows(0);
+    vm_wait_barrier<0>();
+    setup_load(0);
+    issue(0, std::integral_constant<int, 0>{});
+    issue(1, std::integral_constant<int, 1>{});
+    issue(2, std::integral_constant<int, 2>{});
+
+    Item ci{};     // the compute cursor's item
+    int xrow = 0;  // A row of tile row `lane` (the bias term's X splits)
+    bool no_bias = false;
+    int cn = 0, ks = -1;  // the compute cursor's item and K step
+    u32x4 sch0 = {0u, 0u, 0u, 0u}, sch1 = sch0;  // scales of the current 8-step chunk
+
+    auto step = [&](int gs, auto st_c) __attribute__((always_inline)) {
+        constexpr int ST = decltype(st_c)::value;
+        if (++ks == nks) ks = 0, ++cn;
+        const int younger = min(NS - 2, total_steps - 1 - gs);
+        if (younger >= 2) vm_wait_barrier<8>();
+        else if (younger == 1) vm_wait_barrier<4>();
+        else vm_wait_barrier<0>();
+        if (gs + NS - 1 < total_steps) issue(gs + NS - 1, std::integral_constant<int, (ST + NS - 1) % NS>{});
+
+        if (ST == 0 && ks == 0) {
+            ci = item_of(cn);
+            int x0 = a_row(ci, cn, lane);
+            if (ci.tile >= 0) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x0));
+            xrow = x0;
+            no_bias = ci.sh ? j.sh.w0.biases == nullptr : j.w0.biases == nullptr;
+        }
+        // the bias term: chunk c (entries 8c .. 8c + 7, i.e. groups 8c / H .. of this item) runs
+        // at the last K step of its groups, per (c + 1) - 1, and loads its operands 3 steps before
+        const int axe = ci.sh ? j.sh.ax_e : j.ax_e;
+        const int H = axe == G ? 1 : 2;  // entries per group: 1 (x) or 2 (act: two half-group sums)
+        const int per = 8 / H;           // K steps per chunk: 8 or 4
+        const int c_now = (ks + 1) % per == 0 ? (ks + 1) / per - 1 : -1;
+        const int c_pre = ST == 0 && (ks + 4) % per == 0 ? (ks + 4) / per - 1 : -1;
+        if (c_pre >= 0) {  // the chunk's X splits (waves 0-2) and biases into LDS
+            if (wave < 3) {
+                const bf16_t *AX = ci.sh ? j.sh.AX : j.AX;
+                dma16(AX + ((size_t)xrow * 3 + wave) * axe + 8 * c_pre, smem + OFF_X + wave * 1024);
+            }
+            if (!no_bias) {
+                const int R = tid;  // B row
+                const bool upr = GLU && R >= 128;
+                const int col = ci.n0 + (GLU ? (R & 127) : R);
+                const size_t wrow = (size_t)ci.e * (size_t)(ci.sh ? j.sh.w0.out : j.w0.out) + col;
+                const bf16_t *bg = unip(ci.sh ? j.sh.w0.biases : j.w0.biases);
+                const bf16_t *bu = GLU ? unip(ci.sh ? j.sh.w1.biases : j.w1.biases) : bg;
+                const bf16_t *bi_ = upr ? bu : bg;
+                // the 16-byte aligned 8 groups holding the chunk's groups (H = 2: two chunks)
+                dma16(bi_ + wrow * (size_t)G + (((8 * c_pre) / H) & ~7), smem + OFF_B + wave * 1024);
+            }
+        }
+
+        // ---- the K step: fragments from LDS (stage ST: immediate offsets)
+        constexpr int SA = ST * STAGE, SC = ST * STAGE + A_BYTES;
+        const uint32_t spar = ((gs >> 3) & 1) * S_BYTES;
+        u32x4 cw0 = ds_read16<SC>(c_addr0), cw1 = ds_read16<SC>(c_addr1);
+        u32x4 a00 = ds_read16<SA>(a_off[0]), a10 = ds_read16<SA + 4096>(a_off[0]);
+        u32x4 a01 = ds_read16<SA>(a_off[1]), a11 = ds_read16<SA + 4096>(a_off[1]);
+        u32x4 a02 = ds_read16<SA>(a_off[2]), a12 = ds_read16<SA + 4096>(a_off[2]);
+        u32x4 a03 = ds_read16<SA>(a_off[3]), a13 = ds_read16<SA + 4096>(a_off[3]);
+        if (ST == 0 && (ks & 7) == 0) {  // a new chunk of scales: 8 groups per B row
+            sch0 = ds_read16<0>(s_addr0 + spar);
+            sch1 = ds_read16<0>(s_addr1 + spar);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(cw0), "+v"(cw1), "+v"(sch0), "+v"(sch1), "+v"(a00), "+v"(a10),
+                       "+v"(a01), "+v"(a11), "+v"(a02), "+v"(a12), "+v"(a03), "+v"(a13));
+        const u32x4 af[2][4] = {{a00, a01, a02, a03}, {a10, a11, a12, a13}};
+        const int gi = ks & 7;
+        // one B fragment at a time: its 4 code words expand once and feed both row fragments
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) {
+            const u32x4 cw = ni ? cw1 : cw0;
+            mg_f32x16 part[2];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const mg_bf16x8 bf = __builtin_bit_cast(mg_bf16x8, mg_expand(cw[s], cm, cx));
+#pragma unroll
+                for (int mi = 0; mi < 2; ++mi) {
+                    const mg_bf16x8 a = __builtin_bit_cast(mg_bf16x8, af[mi][s]);
+                    if (s == 0) {
+                        const mg_f32x16 z = {};
+                        part[mi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bf, z, 0, 0, 0);
+                    } else {
+                        part[mi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bf, part[mi], 0, 0, 0);
+                    }
+                }
+            }
+            const u32x4 sw = ni ? sch1 : sch0;
+            const uint32_t w2 = (gi & 4) ? ((gi & 2) ? sw.w : sw.z) : ((gi & 2) ? sw.y : sw.x);
+            const float sc = (gi & 1) ? bf_hi(w2) : bf_lo(w2);
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[mi][ni][i] += sc * part[mi][i];
+        }
+        if (c_now >= 0) {  // bias term of chunk c_now: X splits against b (lane half 0), -128 s (1)
+            const uint32_t xo = lds0 + OFF_X + 16 * fr;
+            u32x4 xa00 = ds_read16<0>(xo), xa01 = ds_read16<1024>(xo), xa02 = ds_read16<2048>(xo);
+            u32x4 xa10 = ds_read16<512>(xo), xa11 = ds_read16<1536>(xo), xa12 = ds_read16<2560>(xo);
+            u32x4 bv0 = ds_read16<0>(lds0 + OFF_B + (uint32_t)(bro0 + fr) * 16);
+            u32x4 bv1 = ds_read16<0>(lds0 + OFF_B + (uint32_t)(bro1 + fr) * 16);
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(xa00), "+v"(xa01), "+v"(xa02), "+v"(xa10), "+v"(xa11), "+v"(xa12),
+                           "+v"(bv0), "+v"(bv1));
+            const u32x4 xa[2][3] = {{xa00, xa01, xa02}, {xa10, xa11, xa12}};
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) {
+                // lane half 0: the biases; lane half 1: -128 x the scales of this K chunk
+                u32x4 v = fh == 0 ? (ni ? bv1 : bv0) : (ni ? sch1 : sch0);
+                if (H == 2) {  // entries 2g, 2g + 1 (two half-group sums) share group g's value
+                    const uint32_t g01 = (c_now & 1) ? v.z : v.x, g23 = (c_now & 1) ? v.w : v.y;
+                    v.x = __builtin_amdgcn_perm(g01, g01, 0x01000100u);
+                    v.y = __builtin_amdgcn_perm(g01, g01, 0x03020302u);
+                    v.z = __builtin_amdgcn_perm(g23, g23, 0x01000100u);
+                    v.w = __builtin_amdgcn_perm(g23, g23, 0x03020302u);
+                }
+                if (fh == 1) {
+                    v.x = mg_neg128(v.x), v.y = mg_neg128(v.y);
+                    v.z = mg_neg128(v.z), v.w = mg_neg128(v.w);
+                } else if (no_bias) {
+                    v = u32x4{0u, 0u, 0u, 0u};
+                }
+#pragma unroll
+                for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                    for (int tt = 0; tt < 3; ++tt)
+                        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                            __builtin_bit_cast(mg_bf16x8, xa[mi][tt]),
+                            __builtin_bit_cast(mg_bf16x8, v), acc[mi][ni], 0, 0, 0);
+            }
+        }
+        if (ST != 3 || ks != nks - 1) return;
+
+        // ---- epilogue of item ci. Stores are widened by exchanging values between lanes (DPP):
+        // a 2-byte store per lane and value costs about as much as a 16-byte one.
+        bf16_t *out = ci.sh ? j.sh.out : j.out;
+        const int ldo = ci.sh ? j.sh.ldo : j.ldo;
+        if (GLU) {
+            // act = R(silu(R(gate)) * R(up)), stored packed; and this wave's half-group sums of
+            // the act rows (their X split) for the down product
+            bf16_t *OX = ci.sh ? j.sh.OX : j.OX;
+            const int oxe = 2 * (j.N / 64);
+            const int col = ci.n0 + wave * 32 + fr;
+            const int c64 = col & 63, kb = c64 >> 3, jj = c64 & 7;
+            // lanes with jj < 4 store packed pair (jj, jj + 4) of rows i (i even); lanes jj >= 4
+            // the pair of row i + 1: both at the packed position of jj & 3
+            const int pcol = (col & ~63) + 8 * (2 * (kb & 3) + (kb >> 2)) + 2 * (jj & 3);
+            const bool hi4 = (jj & 4) != 0;
+            const int entry = 2 * (col >> 6) + (wave & 1);
+            float xsum = 0.f;  // the half-group sum of tile row `lane`
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int i = 0; i < 16; i += 2) {
+                    uint32_t h[2];
+                    float sum2[2];
+#pragma unroll
+                    for (int d = 0; d < 2; ++d) {
+                        const float g = rbf(acc[mi][0][i + d]), u = rbf(acc[mi][1][i + d]);
+                        // silu(g) = g / (1 + exp(-g)): v_exp and v_rcp (within 2 f32 ulp)
+                        const float e = __builtin_amdgcn_exp2f(-1.44269504088896f * g);
+                        const float v = rbf((g * __builtin_amdgcn_rcpf(1.f + e)) * u);
+                        h[d] = __float_as_uint(v) >> 16;
+                        // sum over the 32 columns of this lane half: rows of 16 lanes, row pairs
+                        float sm = row_sum16(v);
+                        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x142,
+                                                                         0xA, 0xF, false));
+                        sum2[d] = sm;
+                    }
+                    // lane l (jj < 4) keeps row i of (jj, jj + 4); lane l + 4 row i + 1
+                    const uint32_t send = hi4 ? h[0] : h[1];
+                    const uint32_t from_up = (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0x104, 0xF, 0xF, false);   // lane l + 4
+                    const uint32_t from_dn = (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0x114, 0xF, 0xF, false);   // lane l - 4
+                    const uint32_t pair = hi4 ? (from_dn | (h[1] << 16)) : (h[0] | (from_up << 16));
+                    const int r = mi * 32 + 8 * (i >> 2) + 4 * fh + (i & 3) + (hi4 ? 1 : 0);
+                    if (r < ci.mrows)
+                        *(uint32_t *)(out + (size_t)(ci.row0 + r) * ldo + pcol) = pair;
+                    // row sums: lanes 16-31 hold the lane-half-0 rows, 48-63 the lane-half-1 rows
+#pragma unroll
+                    for (int d = 0; d < 2; ++d) {
+                        const int r0 = mi * 32 + 8 * ((i + d) >> 2) + ((i + d) & 3);
+                        const int s0 = __builtin_amdgcn_readlane(__float_as_int(sum2[d]), 16);
+                        const int s1 = __builtin_amdgcn_readlane(__float_as_int(sum2[d]), 48);
+                        int xs = __float_as_int(xsum);
+                        asm("v_writelane_b32 %0, %1, %2" : "+v"(xs) : "s"(s0), "i"(r0));
+                        asm("v_writelane_b32 %0, %1, %2" : "+v"(xs) : "s"(s1), "i"(r0 + 4));
+                        xsum = __int_as_float(xs);
+                    }
+                }
+            if (lane < ci.mrows) {
+                uint32_t hi, mid, lo;
+                split3(xsum, hi, mid, lo);
+                bf16_t *d = OX + (size_t)(ci.row0 + lane) * 3 * oxe + entry;
+                d[0] = (bf16_t)hi;
+                d[oxe] = (bf16_t)mid;
+                d[2 * oxe] = (bf16_t)lo;
+            }
+        } else {
+            // each 4 x 4 block (4 rows of a lane, 4 columns of a lane quad) is transposed within
+            // the quad, so every lane stores 4 adjacent columns of one row (8 bytes)
+            const int q = fr & 3;
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) {
+                const int col4 = ci.n0 + (ni ? bro1 : bro0) + (fr & ~3);
+#pragma unroll
+                for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        const uint32_t h0 = f2bf(acc[mi][ni][4 * b]), h1 = f2bf(acc[mi][ni][4 * b + 1]);
+                        const uint32_t h2 = f2bf(acc[mi][ni][4 * b + 2]), h3 = f2bf(acc[mi][ni][4 * b + 3]);
+                        const uint32_t p02 = h0 | (h2 << 16), p13 = h1 | (h3 << 16);
+                        // lanes q, q ^ 1: even lanes gather rows 0 and 2, odd lanes rows 1 and 3
+                        const uint32_t own = (q & 1) ? p13 : p02;
+                        const uint32_t rcv = (uint32_t)__builtin_amdgcn_mov_dpp((int)((q & 1) ? p02 : p13), 0xB1, 0xF, 0xF, false);
+                        const uint32_t lo_src = (q & 1) ? rcv : own, hi_src = (q & 1) ? own : rcv;
+                        const uint32_t A = __builtin_amdgcn_perm(hi_src, lo_src, 0x05040100u);  // row q & 1
+                        const uint32_t B = __builtin_amdgcn_perm(hi_src, lo_src, 0x07060302u);  // row 2 + (q & 1)
+                        // lanes q, q ^ 2: lanes 0, 1 complete rows 0, 1; lanes 2, 3 rows 2, 3
+                        const uint32_t r2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)((q & 2) ? A : B), 0x4E, 0xF, 0xF, false);
+                        const uint2 w = (q & 2) ? make_uint2(r2, B) : make_uint2(A, r2);
+                        const int r = mi * 32 + 8 * b + 4 * fh + q;
+                        if (r < ci.mrows) *(uint2 *)(out + (size_t)(ci.row0 + r) * ldo + col4) = w;
+                    }
+            }
+        }
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[mi][ni][i] = 0.f;
+    };
+    // each K step is scheduled on its own (sched_barrier): interleaving neighbouring steps only
+    // lengthens live ranges past the register budget of two waves per SIMD
+    for (int gs = 0; gs < total_steps; gs += NS) {
+        step(gs, std::integral_constant<int, 0>{});
+        __builtin_amdgcn_sched_barrier(0);
+        step(gs + 1, std::integral_constant<int, 1>{});
+        __builtin_amdgcn_sched_barrier(0);
+        step(gs + 2, std::integral_constant<int, 2>{});
+        __builtin_amdgcn_sched_barrier(0);
+        step(gs + 3, std::integral_constant<int, 3>{});
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+bool moe_gemm_supported(const MoeGemmJob &j) {
+    auto ok = [](const QW &w, int K) {
+        // byte offsets from the tensors' bases are 32-bit
+        return w.codes && w.scales && w.bits == 4 && w.group == 64 && K % 512 == 0 &&
+               (size_t)w.experts * (size_t)w.out * (size_t)(K / 2) < ((size_t)1 << 32) &&
+               ((uintptr_t)w.codes & 15) == 0 && ((uintptr_t)w.scales & 15) == 0 &&
+               (!w.biases || ((uintptr_t)w.biases & 15) == 0);
+    };
+    const int ncols = j.glu ? 128 : 256;
+    if (j.N <= 0 || j.N % ncols != 0 || !ok(j.w0, j.K) || (j.glu && !ok(j.w1, j.K))) return false;
+    if (j.w0.out != j.N || (j.glu && j.w1.out != j.N)) return false;
+    if (j.ax_e % 8 != 0 || (j.ax_e != j.K / 64 && j.ax_e != 2 * (j.K / 64))) return false;
+    if (j.has_shared) {
+        if (!ok(j.sh.w0, j.K) || (j.glu && !ok(j.sh.w1, j.K))) return false;
+        if (j.sh.w0.out != j.N || (j.glu && j.sh.w1.out != j.N)) return false;
+        if (j.sh.ax_e % 8 != 0 || (j.sh.ax_e != j.K / 64 && j.sh.ax_e != 2 * (j.K / 64)))
+            return false;
+    }
+    return true;
+}
+
+static int cu_count() {
+    static int cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+hipError_t launch_moe_gemm(const MoeGemmJob &j, hipStream_t stream) {
+    if (!moe_gemm_supported(j)) return hipErrorInvalidValue;
+    const int ncols = j.glu ? 128 : 256;
+    const int nb = j.N / ncols;
+    const int s_tiles = j.has_shared ? (j.sh.M + mg::BM - 1) / mg::BM : 0;
+    const int r_tiles = j.has_routing ? j.max_tiles : (j.M + mg::BM - 1) / mg::BM;
+    const long long items = (long long)(s_tiles + r_tiles) * nb;
+    if (items == 0) return hipSuccess;
+    long long grid = 2LL * cu_count();
+    if (grid > items) grid = items;
+    grid = (grid + 7) / 8 * 8;
+    if (j.glu) moe_gemm_kernel<true><<<(unsigned)grid, mg::NT, 0, stream>>>(j);
+    else moe_gemm_kernel<false><<<(unsigned)grid, mg::NT, 0, stream>>>(j);
+    return hipGetLastError();
+}
+
+}  // namespace mrun

@@ -89,7 +89,7 @@ __global__ __launch_bounds__(1024) void route_scatter_kernel(const uint32_t *__r
                                                              PermuteOut o) {
     __shared__ uint32_t bm[8192];        // [E][W] pair bitmaps of this block
     __shared__ uint32_t part[2][1024];   // per (split, expert): pairs before this block, all pairs
-    __shared__ uint32_t base[1024], tmp[32];
+    __shared__ uint32_t base[1024], tbase[1024], eoff[1024], ecnt[1024], tmp[32];
     const int tid = threadIdx.x, b = blockIdx.x;
     const int W = (BP + 31) / 32;
     for (int i = tid; i < E * W; i += 1024) bm[i] = 0;
@@ -122,6 +122,12 @@ __global__ __launch_bounds__(1024) void route_scatter_kernel(const uint32_t *__r
     uint32_t total;
     const uint32_t ex = block_exclusive_scan<1024>(cnt, tmp, &total);  // (barriers inside)
     if (tid < E) base[tid] = ex + bef;
+    // first tile of each expert (tiles of tile_m rows), for the tile row lists
+    const uint32_t m = (uint32_t)o.tile_m;
+    const uint32_t nt = m ? (cnt + m - 1) / m : 0u;
+    uint32_t n_tiles = 0;
+    const uint32_t b0 = block_exclusive_scan<1024>(nt, tmp, &n_tiles);
+    if (tid < E) tbase[tid] = b0, eoff[tid] = ex, ecnt[tid] = cnt;
     __syncthreads();
     if (my_e < (uint32_t)E) {
         const uint32_t *row = bm + my_e * W;
@@ -132,6 +138,13 @@ __global__ __launch_bounds__(1024) void route_scatter_kernel(const uint32_t *__r
         if (o.order) o.order[pos] = p;
         if (o.inverse) o.inverse[p] = pos;
         if (o.token) o.token[pos] = p / (uint32_t)k;
+        if (o.tile_rows) {  // the token of each tile row; a partial tile repeats its last row
+            const uint32_t in_e = pos - eoff[my_e];
+            uint32_t *tr = o.tile_rows + (size_t)(tbase[my_e] + in_e / m) * m;
+            tr[in_e % m] = p / (uint32_t)k;
+            if (in_e + 1 == ecnt[my_e])
+                for (uint32_t rr = in_e % m + 1; rr < m; ++rr) tr[rr] = p / (uint32_t)k;
+        }
     }
     if (b != 0) return;
     if (tid < E) o.offsets[tid] = ex;
@@ -142,9 +155,6 @@ __global__ __launch_bounds__(1024) void route_scatter_kernel(const uint32_t *__r
         if (tid == 0) *o.n_active = total;
     }
     if (o.tiles) {
-        const uint32_t m = (uint32_t)o.tile_m;
-        const uint32_t nt = (cnt + m - 1) / m;
-        const uint32_t b0 = block_exclusive_scan<1024>(nt, tmp, &total);
         if (tid < E)
             for (uint32_t i = 0; i < nt; ++i) {
                 uint32_t *t3 = o.tiles + 3 * (size_t)(b0 + i);
@@ -152,7 +162,7 @@ __global__ __launch_bounds__(1024) void route_scatter_kernel(const uint32_t *__r
                 t3[1] = ex + i * m;
                 t3[2] = min(m, cnt - i * m);
             }
-        if (tid == 0) *o.n_tiles = total;
+        if (tid == 0) *o.n_tiles = n_tiles;
     }
 }
 
