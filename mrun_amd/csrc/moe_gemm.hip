@@ -74,13 +74,19 @@ __device__ __forceinline__ uint32_t ds_read2(uint32_t a) {
     asm volatile("ds_read_u16 %0, %1" : "=v"(v) : "v"(a));
     return v;
 }
-// 16 (or 4) bytes per lane from global memory into LDS at lds + 16 * lane (4 * lane): the LDS
-// address must be the same for the whole wave.
-__device__ __forceinline__ void dma16(const void *g, char *lds) {
-    __builtin_amdgcn_global_load_lds(g, (lds_void_t *)lds, 16, 0, 0);
+// Global memory goes to LDS through buffer loads (buffer_load ... lds): a raw resource per
+// tensor (base address in scalar registers), a per-lane 32-bit byte offset and a scalar one, so
+// that no per-lane 64-bit address arithmetic is needed. 16 (or 4) bytes per lane land at
+// lds + 16 * lane (4 * lane); the LDS address is the same for the whole wave.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t rsrc_of(const void *p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, (int)0xFFFFFFFFu, 0x00020000);
 }
-__device__ __forceinline__ void dma4(const void *g, char *lds) {
-    __builtin_amdgcn_global_load_lds(g, (lds_void_t *)lds, 4, 0, 0);
+__device__ __forceinline__ void dma16(rsrc_t r, uint32_t voff, uint32_t soff, char *lds) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)lds, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void dma4(rsrc_t r, uint32_t voff, uint32_t soff, char *lds) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)lds, 4, voff, soff, 0, 0);
 }
 // Wait until at most N of this wave's global loads are outstanding, then a workgroup barrier.
 template <int N>
@@ -88,13 +94,14 @@ __device__ __forceinline__ void vm_wait_barrier() {
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"i"(N) : "memory");
 }
 
-__device__ __forceinline__ u32x4 mg_expand(uint32_t w, uint32_t cm, uint32_t cx) {
-    u32x4 r;
+// a code word (8 codes) into the bf16 pairs (128 + q_i, 128 + q_{i+4}), in two halves
+__device__ __forceinline__ void mg_expand_lo(u32x4 &r, uint32_t w, uint32_t cm, uint32_t cx) {
     r.x = (w & cm) | cx;
     r.y = ((w >> 4) & cm) | cx;
+}
+__device__ __forceinline__ void mg_expand_hi(u32x4 &r, uint32_t w, uint32_t cm, uint32_t cx) {
     r.z = ((w >> 8) & cm) | cx;
     r.w = ((w >> 12) & cm) | cx;
-    return r;
 }
 
 // -128 s for a pair of bf16 scales (exact: a power-of-two scaling)
@@ -186,11 +193,17 @@ __device__ __forceinline__ void tile_record(const uint32_t *t3, int &e, int &row
     e = (int)(uint32_t)ab, row0 = (int)(uint32_t)(ab >> 32), mrows = (int)c;
 }
 
+// LDS swizzles. A rows are 128 B (8 units): rows r and r + 8 (same bank window at 256 B per
+// cycle) and rows of one parity in 16 get distinct masks. B rows are 32 B (2 units): rows r and
+// r + 4 (128-byte window) and r and r + 8 (256-byte window) get distinct masks.
+__device__ __forceinline__ int swz_a(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int swz_c(int r) { return ((r >> 2) ^ (r >> 3)) & 1; }
+
 template <bool GLU>
 __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
     using namespace mg;
     __shared__ __align__(16) char smem[LDS_BYTES];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = uni(tid >> 6);
     const int fr = lane & 31, fh = lane >> 5;
     const uint32_t lds0 = lds_offset(smem);
     char *const rowbuf = smem + OFF_R;
@@ -236,15 +249,15 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
     };
 
     // ---- load role: A rows ra, ra + 32 (16-byte unit ua), B rows rb, rb + 128 (unit uc), scale
-    // row tid. Units are XOR-swizzled so that the fragment reads of 8 lanes (a 128-byte LDS
-    // cycle) fall on distinct banks: A unit u of row r sits at u ^ (r & 7), code unit u of B row R
-    // at u ^ ((R >> 2) & 1).
+    // row tid. Units are XOR-swizzled (swz_a, swz_c) so that the 16-byte fragment reads of 16
+    // adjacent lanes fall on distinct 16-byte bank groups of a 256-byte window, and those of 8
+    // adjacent lanes on distinct ones of a 128-byte window.
     const int ra = wave * 8 + (lane >> 3);
-    const uint32_t ua16 = 16u * (uint32_t)((lane & 7) ^ (ra & 7));
+    const uint32_t ua16 = 16u * (uint32_t)((lane & 7) ^ swz_a(ra));
     const int rb = tid >> 1;
-    const uint32_t uc16 = 16u * (uint32_t)((tid & 1) ^ ((rb >> 2) & 1));
-    // byte offsets of this lane's DMA sources from the item's (scalar) base pointers
-    const char *a_base = nullptr, *c_base0 = nullptr, *c_base1 = nullptr, *s_base = nullptr;
+    const uint32_t uc16 = 16u * (uint32_t)((tid & 1) ^ swz_c(rb));
+    // the item's sources and this lane's byte offsets in them
+    rsrc_t r_a, r_c0, r_c1, r_s;
     uint32_t la0 = 0, la1 = 0, lc0 = 0, lc1 = 0, ls = 0;
     int l_item = 0, l_ks = 0;
 
@@ -259,42 +272,49 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
         if (n >= n_items || wave != 0) return;
         const Item it = item_of(n);
         if (it.tile < 0) return;
-        dma4(j.tile_rows + (size_t)it.tile * BM + lane, rowbuf + (n % 3) * R_BYTES);
+        dma4(rsrc_of(j.tile_rows), 4u * (uint32_t)lane, 4u * (uint32_t)(it.tile * BM),
+             rowbuf + (n % 3) * R_BYTES);
     };
     auto setup_load = [&](int n) __attribute__((always_inline)) {
         const Item it = item_of(n);
         int r0 = a_row(it, n, ra), r1 = a_row(it, n, ra + 32);
         if (it.tile >= 0) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r0), "+v"(r1));
         const int lda = it.sh ? j.sh.lda : j.lda;
-        a_base = (const char *)(it.sh ? j.sh.A : j.A);
+        r_a = rsrc_of(it.sh ? j.sh.A : j.A);
         la0 = (uint32_t)r0 * (uint32_t)lda * 2u + ua16;
         la1 = (uint32_t)r1 * (uint32_t)lda * 2u + ua16;
-        c_base0 = (const char *)(it.sh ? j.sh.w0.codes : j.w0.codes);
-        c_base1 = GLU ? (const char *)(it.sh ? j.sh.w1.codes : j.w1.codes) : c_base0;
+        r_c0 = rsrc_of(it.sh ? j.sh.w0.codes : j.w0.codes);
+        r_c1 = GLU ? rsrc_of(it.sh ? j.sh.w1.codes : j.w1.codes) : r_c0;
         const uint32_t wrow = (uint32_t)it.e * (uint32_t)(it.sh ? j.sh.w0.out : j.w0.out);
         const uint32_t col0 = (uint32_t)(it.n0 + rb), col1 = GLU ? col0 : col0 + 128u;
         lc0 = (wrow + col0) * (uint32_t)(K / 2) + uc16;
         lc1 = (wrow + col1) * (uint32_t)(K / 2) + uc16;
-        const bool up = GLU && tid >= 128;
-        const char *sg = (const char *)unip(it.sh ? j.sh.w0.scales : j.w0.scales);
-        const char *su = GLU ? (const char *)unip(it.sh ? j.sh.w1.scales : j.w1.scales) : sg;
-        s_base = up ? su : sg;
+        const bool up = GLU && wave >= 2;  // waves 2, 3 load the up rows' scales
+        r_s = rsrc_of(up ? (it.sh ? j.sh.w1.scales : j.w1.scales) : (it.sh ? j.sh.w0.scales : j.w0.scales));
         ls = (wrow + (uint32_t)(GLU ? it.n0 + (tid & 127) : it.n0 + tid)) * (uint32_t)G * 2u;
         fetch_rows(n + 1);  // one item ahead
     };
     // issue the DMA of global step gl (the load cursor's item and K step) into ring stage ST
-    auto issue = [&](int gl, auto st_c) __attribute__((always_inline)) {
+    // copy `part` of global step gl (the load cursor's item and K step) into ring stage ST:
+    // A rows ra (0), ra + 32 (1), B rows rb (2), rb + 128 (3), and the scale chunk with part 0
+    auto issue_part = [&](int gl, int part, auto st_c) __attribute__((always_inline)) {
         constexpr int ST = decltype(st_c)::value;
         char *sa = smem + ST * STAGE, *sc = sa + A_BYTES;
         // nks is a multiple of 8 and the stream starts at step 0 of an item, so a chunk of
         // scales can only start at ring stage 0 and an item can only end at ring stage 3
-        if constexpr (ST == 0)
-            if ((l_ks & 7) == 0)  // the scale chunk of K steps l_ks .. l_ks + 7
-                dma16(s_base + ls + 2 * l_ks, smem + OFF_S + ((gl >> 3) & 1) * S_BYTES + wave * 1024);
-        dma16(a_base + la0 + l_ks * 128, sa + wave * 1024);
-        dma16(a_base + la1 + l_ks * 128, sa + 4096 + wave * 1024);
-        dma16(c_base0 + lc0 + l_ks * 32, sc + wave * 1024);
-        dma16(c_base1 + lc1 + l_ks * 32, sc + 4096 + wave * 1024);
+        if (part == 0) {
+            if constexpr (ST == 0)
+                if ((l_ks & 7) == 0)  // the scale chunk of K steps l_ks .. l_ks + 7
+                    dma16(r_s, ls, 2u * l_ks, smem + OFF_S + ((gl >> 3) & 1) * S_BYTES + wave * 1024);
+            dma16(r_a, la0, 128u * l_ks, sa + wave * 1024);
+        }
+        if (part == 1) dma16(r_a, la1, 128u * l_ks, sa + 4096 + wave * 1024);
+        if (part == 2) dma16(r_c0, lc0, 32u * l_ks, sc + wave * 1024);
+        if (part == 3) dma16(r_c1, lc1, 32u * l_ks, sc + 4096 + wave * 1024);
+    };
+    // the load cursor's next K step (and item)
+    auto advance = [&](auto st_c) __attribute__((always_inline)) {
+        constexpr int ST = decltype(st_c)::value;
         ++l_ks;
         if constexpr (ST == 3)
             if (l_ks == nks) {
@@ -302,13 +322,17 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
                 if (++l_item < n_items) setup_load(l_item);
             }
     };
+    auto issue = [&](int gl, auto st_c) __attribute__((always_inline)) {
+        for (int part = 0; part < 4; ++part) issue_part(gl, part, st_c);
+        advance(st_c);
+    };
 
     // ---- compute role: rows mi * 32 + fr, B rows bro[ni] + fr
     uint32_t a_off[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-        a_off[s] = lds0 + (uint32_t)(fr * 128 + 16 * ((2 * s + fh) ^ (fr & 7)));
-    const uint32_t c_off = (uint32_t)(fr * 32 + 16 * (fh ^ ((fr >> 2) & 1)));
+        a_off[s] = lds0 + (uint32_t)(fr * 128 + 16 * ((2 * s + fh) ^ swz_a(fr)));
+    const uint32_t c_off = (uint32_t)(fr * 32 + 16 * (fh ^ swz_c(fr)));
     const int bro0 = GLU ? wave * 32 : wave * 64, bro1 = GLU ? 128 + wave * 32 : wave * 64 + 32;
     const uint32_t c_addr0 = lds0 + (uint32_t)bro0 * 32 + c_off, c_addr1 = lds0 + (uint32_t)bro1 * 32 + c_off;
     const uint32_t s_addr0 = lds0 + OFF_S + (uint32_t)(bro0 + fr) * 16;
@@ -337,6 +361,12 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
     bool no_bias = false;
     int cn = 0, ks = -1;  // the compute cursor's item and K step
     u32x4 sch0 = {0u, 0u, 0u, 0u}, sch1 = sch0;  // scales of the current 8-step chunk
+    mg_f32x16 part0[2], part1[2];  // the K step's group products P' of fragments 0 and 1
+    float sc_pend = 0.f;           // scale still to apply to part1
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) part0[mi][i] = part1[mi][i] = 0.f;
 
     auto step = [&](int gs, auto st_c) __attribute__((always_inline)) {
         constexpr int ST = decltype(st_c)::value;
@@ -345,7 +375,9 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
         if (younger >= 2) vm_wait_barrier<8>();
         else if (younger == 1) vm_wait_barrier<4>();
         else vm_wait_barrier<0>();
-        if (gs + NS - 1 < total_steps) issue(gs + NS - 1, std::integral_constant<int, (ST + NS - 1) % NS>{});
+        // this step's copies (NS - 1 steps ahead) are issued between its MFMAs
+        const bool copies = gs + NS - 1 < total_steps;
+        constexpr auto ST_L = std::integral_constant<int, (ST + NS - 1) % NS>{};
 
         if (ST == 0 && ks == 0) {
             ci = item_of(cn);
@@ -356,73 +388,103 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
         }
         // the bias term: chunk c (entries 8c .. 8c + 7, i.e. groups 8c / H .. of this item) runs
         // at the last K step of its groups, per (c + 1) - 1, and loads its operands 3 steps before
-        const int axe = ci.sh ? j.sh.ax_e : j.ax_e;
-        const int H = axe == G ? 1 : 2;  // entries per group: 1 (x) or 2 (act: two half-group sums)
-        const int per = 8 / H;           // K steps per chunk: 8 or 4
+        constexpr int H = GLU ? 1 : 2;  // entries per group: 1 (x) or 2 (act: two half-group sums)
+        constexpr int per = 8 / H;       // K steps per chunk: 8 or 4
+        const int axe = H * G;
         const int c_now = (ks + 1) % per == 0 ? (ks + 1) / per - 1 : -1;
         const int c_pre = ST == 0 && (ks + 4) % per == 0 ? (ks + 4) / per - 1 : -1;
         if (c_pre >= 0) {  // the chunk's X splits (waves 0-2) and biases into LDS
-            if (wave < 3) {
-                const bf16_t *AX = ci.sh ? j.sh.AX : j.AX;
-                dma16(AX + ((size_t)xrow * 3 + wave) * axe + 8 * c_pre, smem + OFF_X + wave * 1024);
-            }
+            if (wave < 3)
+                dma16(rsrc_of(ci.sh ? j.sh.AX : j.AX), 2u * (uint32_t)((xrow * 3 + wave) * axe),
+                      16u * (uint32_t)c_pre, smem + OFF_X + wave * 1024);
             if (!no_bias) {
                 const int R = tid;  // B row
-                const bool upr = GLU && R >= 128;
+                const bool upr = GLU && wave >= 2;
                 const int col = ci.n0 + (GLU ? (R & 127) : R);
-                const size_t wrow = (size_t)ci.e * (size_t)(ci.sh ? j.sh.w0.out : j.w0.out) + col;
-                const bf16_t *bg = unip(ci.sh ? j.sh.w0.biases : j.w0.biases);
-                const bf16_t *bu = GLU ? unip(ci.sh ? j.sh.w1.biases : j.w1.biases) : bg;
-                const bf16_t *bi_ = upr ? bu : bg;
+                const uint32_t wrow = (uint32_t)ci.e * (uint32_t)(ci.sh ? j.sh.w0.out : j.w0.out) + col;
+                const bf16_t *bg = ci.sh ? j.sh.w0.biases : j.w0.biases;
+                const bf16_t *bu = GLU ? (ci.sh ? j.sh.w1.biases : j.w1.biases) : bg;
                 // the 16-byte aligned 8 groups holding the chunk's groups (H = 2: two chunks)
-                dma16(bi_ + wrow * (size_t)G + (((8 * c_pre) / H) & ~7), smem + OFF_B + wave * 1024);
+                dma16(rsrc_of(upr ? bu : bg), 2u * wrow * (uint32_t)G,
+                      2u * (uint32_t)(((8 * c_pre) / H) & ~7), smem + OFF_B + wave * 1024);
             }
         }
 
         // ---- the K step: fragments from LDS (stage ST: immediate offsets)
         constexpr int SA = ST * STAGE, SC = ST * STAGE + A_BYTES;
         const uint32_t spar = ((gs >> 3) & 1) * S_BYTES;
-        u32x4 cw0 = ds_read16<SC>(c_addr0), cw1 = ds_read16<SC>(c_addr1);
+        // Reads in the order they are needed; LDS reads complete in order, so a partial lgkmcnt
+        // wait covers the oldest ones (scalar loads in flight only make such waits stricter).
+        u32x4 cw0 = ds_read16<SC>(c_addr0);
         u32x4 a00 = ds_read16<SA>(a_off[0]), a10 = ds_read16<SA + 4096>(a_off[0]);
         u32x4 a01 = ds_read16<SA>(a_off[1]), a11 = ds_read16<SA + 4096>(a_off[1]);
         u32x4 a02 = ds_read16<SA>(a_off[2]), a12 = ds_read16<SA + 4096>(a_off[2]);
         u32x4 a03 = ds_read16<SA>(a_off[3]), a13 = ds_read16<SA + 4096>(a_off[3]);
-        if (ST == 0 && (ks & 7) == 0) {  // a new chunk of scales: 8 groups per B row
+        u32x4 cw1 = ds_read16<SC>(c_addr1);
+        if (ST == 0) {  // the scales of this 8-step chunk: 8 groups per B row
             sch0 = ds_read16<0>(s_addr0 + spar);
             sch1 = ds_read16<0>(s_addr1 + spar);
         }
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(cw0), "+v"(cw1), "+v"(sch0), "+v"(sch1), "+v"(a00), "+v"(a10),
-                       "+v"(a01), "+v"(a11), "+v"(a02), "+v"(a12), "+v"(a03), "+v"(a13));
-        const u32x4 af[2][4] = {{a00, a01, a02, a03}, {a10, a11, a12, a13}};
-        const int gi = ks & 7;
-        // one B fragment at a time: its 4 code words expand once and feed both row fragments
+        constexpr int NR = ST == 0 ? 12 : 10;
+        // the group's scale: ks % 4 == ST (items have a multiple of 8 K steps)
+        const int gi = (ks & 4) | ST;
+        auto scale_of = [&](const u32x4 &sw) __attribute__((always_inline)) {
+            const uint32_t w2 = (gi & 4) ? ((ST & 2) ? sw.w : sw.z) : ((ST & 2) ? sw.y : sw.x);
+            return (ST & 1) ? bf_hi(w2) : bf_lo(w2);
+        };
+        // The matrix cores run fragment 0's chains, then fragment 1's (4 K sub-steps x 2 row
+        // fragments each). Between two MFMAs the wave issues about 7 VALU: the expansion of the
+        // next code word and 4 scale FMAs, those of fragment 1 of the previous K step (pend)
+        // under fragment 0's chains, and fragment 0's under fragment 1's, so that no FMA waits
+        // for the chain it reads. sched_barrier pins the interleave.
+        u32x4 e = {0u, 0u, 0u, 0u}, en = e;
+        float sc0 = 0.f;
+        asm volatile("s_waitcnt lgkmcnt(%3)" : "+v"(cw0), "+v"(a00), "+v"(a10) : "i"(NR - 3));
+        mg_expand_lo(e, cw0[0], cm, cx);
+        mg_expand_hi(e, cw0[0], cm, cx);
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
-            const u32x4 cw = ni ? cw1 : cw0;
-            mg_f32x16 part[2];
+        for (int q = 0; q < 16; ++q) {  // MFMA slot q: fragment q / 8, sub-step (q / 2) % 4, rows q % 2
+            const int ni = q >> 3, s = (q >> 1) & 3, mi = q & 1;
+            if (q == 2) asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a01), "+v"(a11) : "i"(NR - 5));
+            if (q == 4) asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a02), "+v"(a12) : "i"(NR - 7));
+            if (q == 6) asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a03), "+v"(a13) : "i"(NR - 9));
+            const u32x4 af = mi ? (s == 0 ? a10 : s == 1 ? a11 : s == 2 ? a12 : a13)
+                                : (s == 0 ? a00 : s == 1 ? a01 : s == 2 ? a02 : a03);
+            mg_f32x16 &pt = ni ? part1[mi] : part0[mi];
+            const mg_f32x16 z = {};
+            pt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(mg_bf16x8, af),
+                                                        __builtin_bit_cast(mg_bf16x8, e),
+                                                        s ? pt : z, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if ((q & 3) == 1 && copies) issue_part(gs + NS - 1, q >> 2, ST_L);
+            // 4 scale FMAs: slot q's share of pend (q < 8) or of fragment 0 (q >= 8)
+            if (q == 8) {
+                if (ST == 0) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(sch0), "+v"(sch1));
+                sc0 = scale_of(sch0);
+            }
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const mg_bf16x8 bf = __builtin_bit_cast(mg_bf16x8, mg_expand(cw[s], cm, cx));
-#pragma unroll
-                for (int mi = 0; mi < 2; ++mi) {
-                    const mg_bf16x8 a = __builtin_bit_cast(mg_bf16x8, af[mi][s]);
-                    if (s == 0) {
-                        const mg_f32x16 z = {};
-                        part[mi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bf, z, 0, 0, 0);
-                    } else {
-                        part[mi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bf, part[mi], 0, 0, 0);
-                    }
+            for (int i = 4 * (q & 3); i < 4 * (q & 3) + 4; ++i) {
+                const int fm = (q & 7) >> 2;
+                if (q < 8) acc[fm][1][i] += sc_pend * part1[fm][i];
+                else acc[fm][0][i] += sc0 * part0[fm][i];
+            }
+            // half of the code word of the next (fragment, sub-step) pair nn: the low half after
+            // the pair's first MFMA, the high half after its second, then it becomes the operand
+            const int nn = (q >> 1) + 1;
+            if (nn < 8) {
+                if (q == 6) asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(cw1) : "i"(NR - 10));
+                const uint32_t w = (nn < 4 ? cw0 : cw1)[nn & 3];
+                if ((q & 1) == 0) {
+                    mg_expand_lo(en, w, cm, cx);
+                } else {
+                    mg_expand_hi(en, w, cm, cx);
+                    e = en;
                 }
             }
-            const u32x4 sw = ni ? sch1 : sch0;
-            const uint32_t w2 = (gi & 4) ? ((gi & 2) ? sw.w : sw.z) : ((gi & 2) ? sw.y : sw.x);
-            const float sc = (gi & 1) ? bf_hi(w2) : bf_lo(w2);
-#pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) acc[mi][ni][i] += sc * part[mi][i];
+            __builtin_amdgcn_sched_barrier(0);
         }
+        sc_pend = scale_of(sch1);
+        if (copies) advance(ST_L);
         if (c_now >= 0) {  // bias term of chunk c_now: X splits against b (lane half 0), -128 s (1)
             const uint32_t xo = lds0 + OFF_X + 16 * fr;
             u32x4 xa00 = ds_read16<0>(xo), xa01 = ds_read16<1024>(xo), xa02 = ds_read16<2048>(xo);
@@ -460,6 +522,12 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
             }
         }
         if (ST != 3 || ks != nks - 1) return;
+        // the item's last fragment-1 scale
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[mi][1][i] += sc_pend * part1[mi][i];
+        sc_pend = 0.f;
 
         // ---- epilogue of item ci. Stores are widened by exchanging values between lanes (DPP):
         // a 2-byte store per lane and value costs about as much as a 16-byte one.
@@ -585,12 +653,13 @@ bool moe_gemm_supported(const MoeGemmJob &j) {
     const int ncols = j.glu ? 128 : 256;
     if (j.N <= 0 || j.N % ncols != 0 || !ok(j.w0, j.K) || (j.glu && !ok(j.w1, j.K))) return false;
     if (j.w0.out != j.N || (j.glu && j.w1.out != j.N)) return false;
-    if (j.ax_e % 8 != 0 || (j.ax_e != j.K / 64 && j.ax_e != 2 * (j.K / 64))) return false;
+    // X splits: one entry per group of x for gate/up, two per group of act for down
+    const int axe = (j.glu ? 1 : 2) * (j.K / 64);
+    if (j.ax_e != axe) return false;
     if (j.has_shared) {
         if (!ok(j.sh.w0, j.K) || (j.glu && !ok(j.sh.w1, j.K))) return false;
         if (j.sh.w0.out != j.N || (j.glu && j.sh.w1.out != j.N)) return false;
-        if (j.sh.ax_e % 8 != 0 || (j.sh.ax_e != j.K / 64 && j.sh.ax_e != 2 * (j.K / 64)))
-            return false;
+        if (j.sh.ax_e != axe) return false;
     }
     return true;
 }
