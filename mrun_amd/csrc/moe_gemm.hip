@@ -42,15 +42,18 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 namespace mg {
-constexpr int BM = 64, BK = 64, BNR = 256, NS = 4, NT = 256;
-constexpr int A_BYTES = BM * BK * 2;           // one K step of A: 64 rows x 128 B
-constexpr int C_BYTES = BNR * BK / 2;          // one K step of codes: 256 B rows x 32 B
-constexpr int STAGE = A_BYTES + C_BYTES;
+constexpr int BM = 64, BK = 64, BNR = 256, NT = 256;
+constexpr int KS = 2;                          // K steps per LDS stage
+constexpr int NSTG = 2;                        // stages in the ring
+constexpr int A_STEP = BM * BK * 2;            // one K step of A: 64 rows x 128 B
+constexpr int A_BYTES = KS * A_STEP;
+constexpr int C_BYTES = BNR * 32 * KS;         // codes of a stage: 256 B rows x 64 B
+constexpr int STAGE = A_BYTES + C_BYTES;       // 32 KB
 constexpr int S_BYTES = BNR * 16;              // scales of 8 groups per B row
 constexpr int R_BYTES = BM * 4;                // A rows (tokens) of a routed tile
 constexpr int X_BYTES = BM * 3 * 16;           // bias term: X splits of 8 entries per row
 constexpr int B_BYTES = BNR * 16;              // bias term: biases of 8 groups per B row
-constexpr int OFF_S = NS * STAGE, OFF_R = OFF_S + 2 * S_BYTES, OFF_X = OFF_R + 3 * R_BYTES;
+constexpr int OFF_S = NSTG * STAGE, OFF_R = OFF_S + 2 * S_BYTES, OFF_X = OFF_R + 3 * R_BYTES;
 constexpr int OFF_B = OFF_X + X_BYTES;
 constexpr int LDS_BYTES = OFF_B + B_BYTES;     // 81,664: two workgroups per CU
 }  // namespace mg
@@ -193,11 +196,13 @@ __device__ __forceinline__ void tile_record(const uint32_t *t3, int &e, int &row
     e = (int)(uint32_t)ab, row0 = (int)(uint32_t)(ab >> 32), mrows = (int)c;
 }
 
-// LDS swizzles. A rows are 128 B (8 units): rows r and r + 8 (same bank window at 256 B per
-// cycle) and rows of one parity in 16 get distinct masks. B rows are 32 B (2 units): rows r and
-// r + 4 (128-byte window) and r and r + 8 (256-byte window) get distinct masks.
+// LDS swizzles (16-byte units). A rows are 128 B (8 units): rows r and r + 8 (same bank window
+// at 256 B per cycle) and rows of one parity in 16 get distinct masks. B rows are 64 B (4 units,
+// two K steps of codes): the 4 rows of a 256-byte window... rows r, r + 4, r + 8, r + 12 (which
+// share a position in a 256-byte window) get distinct masks, and so do r, r + 2, r + 4, r + 6
+// (a 128-byte window).
 __device__ __forceinline__ int swz_a(int r) { return (r & 7) ^ ((r >> 3) & 1); }
-__device__ __forceinline__ int swz_c(int r) { return ((r >> 2) ^ (r >> 3)) & 1; }
+__device__ __forceinline__ int swz_c(int r) { return ((r >> 2) ^ (r >> 1)) & 3; }
 
 template <bool GLU>
 __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
@@ -254,11 +259,12 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
     // adjacent lanes on distinct ones of a 128-byte window.
     const int ra = wave * 8 + (lane >> 3);
     const uint32_t ua16 = 16u * (uint32_t)((lane & 7) ^ swz_a(ra));
-    const int rb = tid >> 1;
-    const uint32_t uc16 = 16u * (uint32_t)((tid & 1) ^ swz_c(rb));
+    // codes: copy i moves B rows 64 i + 16 wave + lane / 4, 16-byte unit lane % 4 of each
+    const int rb = 16 * wave + (lane >> 2);
+    const uint32_t uc16 = 16u * (uint32_t)((lane & 3) ^ swz_c(rb));  // swz_c(rb + 64 i) == swz_c(rb)
     // the item's sources and this lane's byte offsets in them
     rsrc_t r_a, r_c0, r_c1, r_s;
-    uint32_t la0 = 0, la1 = 0, lc0 = 0, lc1 = 0, ls = 0;
+    uint32_t la0 = 0, la1 = 0, lc[4] = {0u, 0u, 0u, 0u}, ls = 0;
     int l_item = 0, l_ks = 0;
 
     // the A row (token) of tile row r of item n
@@ -286,45 +292,44 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
         r_c0 = rsrc_of(it.sh ? j.sh.w0.codes : j.w0.codes);
         r_c1 = GLU ? rsrc_of(it.sh ? j.sh.w1.codes : j.w1.codes) : r_c0;
         const uint32_t wrow = (uint32_t)it.e * (uint32_t)(it.sh ? j.sh.w0.out : j.w0.out);
-        const uint32_t col0 = (uint32_t)(it.n0 + rb), col1 = GLU ? col0 : col0 + 128u;
-        lc0 = (wrow + col0) * (uint32_t)(K / 2) + uc16;
-        lc1 = (wrow + col1) * (uint32_t)(K / 2) + uc16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {  // under glu, rows 0-127 are gate (w0), 128-255 up (w1)
+            const int R = 64 * i + rb;
+            const uint32_t col = (uint32_t)(it.n0 + (GLU ? (R & 127) : R));
+            lc[i] = (wrow + col) * (uint32_t)(K / 2) + uc16;
+        }
         const bool up = GLU && wave >= 2;  // waves 2, 3 load the up rows' scales
         r_s = rsrc_of(up ? (it.sh ? j.sh.w1.scales : j.w1.scales) : (it.sh ? j.sh.w0.scales : j.w0.scales));
         ls = (wrow + (uint32_t)(GLU ? it.n0 + (tid & 127) : it.n0 + tid)) * (uint32_t)G * 2u;
         fetch_rows(n + 1);  // one item ahead
     };
     // issue the DMA of global step gl (the load cursor's item and K step) into ring stage ST
-    // copy `part` of global step gl (the load cursor's item and K step) into ring stage ST:
-    // A rows ra (0), ra + 32 (1), B rows rb (2), rb + 128 (3), and the scale chunk with part 0
-    auto issue_part = [&](int gl, int part, auto st_c) __attribute__((always_inline)) {
-        constexpr int ST = decltype(st_c)::value;
-        char *sa = smem + ST * STAGE, *sc = sa + A_BYTES;
-        // nks is a multiple of 8 and the stream starts at step 0 of an item, so a chunk of
-        // scales can only start at ring stage 0 and an item can only end at ring stage 3
-        if (part == 0) {
-            if constexpr (ST == 0)
-                if ((l_ks & 7) == 0)  // the scale chunk of K steps l_ks .. l_ks + 7
-                    dma16(r_s, ls, 2u * l_ks, smem + OFF_S + ((gl >> 3) & 1) * S_BYTES + wave * 1024);
-            dma16(r_a, la0, 128u * l_ks, sa + wave * 1024);
+    // copy `part` of the load cursor's stage (its item, K steps l_ks, l_ks + 1) into ring slot
+    // SLOT: parts 0-3 A (K step part / 2, rows ra + 32 (part % 2)), parts 4-7 codes copy part - 4
+    auto issue_part = [&](int part, auto slot_c) __attribute__((always_inline)) {
+        constexpr int SLOT = decltype(slot_c)::value;
+        char *sa = smem + SLOT * STAGE, *sc = sa + A_BYTES;
+        if (part < 4) {
+            const int kk = part >> 1;
+            dma16(r_a, (part & 1) ? la1 : la0, 128u * (l_ks + kk),
+                  sa + kk * A_STEP + (part & 1) * 4096 + wave * 1024);
+        } else {
+            const int i = part - 4;
+            dma16(GLU && i >= 2 ? r_c1 : r_c0, lc[i], 32u * l_ks, sc + i * 4096 + wave * 1024);
         }
-        if (part == 1) dma16(r_a, la1, 128u * l_ks, sa + 4096 + wave * 1024);
-        if (part == 2) dma16(r_c0, lc0, 32u * l_ks, sc + wave * 1024);
-        if (part == 3) dma16(r_c1, lc1, 32u * l_ks, sc + 4096 + wave * 1024);
     };
-    // the load cursor's next K step (and item)
-    auto advance = [&](auto st_c) __attribute__((always_inline)) {
-        constexpr int ST = decltype(st_c)::value;
-        ++l_ks;
-        if constexpr (ST == 3)
-            if (l_ks == nks) {
-                l_ks = 0;
-                if (++l_item < n_items) setup_load(l_item);
-            }
+    // the scale chunk of K steps l_ks .. l_ks + 7 (global K step gl): items have a multiple of 8 K
+    // steps, so a chunk starts with a ring slot 0 stage
+    auto issue_scales = [&](int gl) __attribute__((always_inline)) {
+        dma16(r_s, ls, 2u * l_ks, smem + OFF_S + ((gl >> 3) & 1) * S_BYTES + wave * 1024);
     };
-    auto issue = [&](int gl, auto st_c) __attribute__((always_inline)) {
-        for (int part = 0; part < 4; ++part) issue_part(gl, part, st_c);
-        advance(st_c);
+    // the load cursor's next stage (and item)
+    auto advance = [&]() __attribute__((always_inline)) {
+        l_ks += KS;
+        if (l_ks == nks) {
+            l_ks = 0;
+            if (++l_item < n_items) setup_load(l_item);
+        }
     };
 
     // ---- compute role: rows mi * 32 + fr, B rows bro[ni] + fr
@@ -332,9 +337,15 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
 #pragma unroll
     for (int s = 0; s < 4; ++s)
         a_off[s] = lds0 + (uint32_t)(fr * 128 + 16 * ((2 * s + fh) ^ swz_a(fr)));
-    const uint32_t c_off = (uint32_t)(fr * 32 + 16 * (fh ^ swz_c(fr)));
     const int bro0 = GLU ? wave * 32 : wave * 64, bro1 = GLU ? 128 + wave * 32 : wave * 64 + 32;
-    const uint32_t c_addr0 = lds0 + (uint32_t)bro0 * 32 + c_off, c_addr1 = lds0 + (uint32_t)bro1 * 32 + c_off;
+    // code words of fragment ni at K step kk of a stage: unit 2 kk + fh of B row bro + fr
+    uint32_t c_addr[2][2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+        const uint32_t off = (uint32_t)(fr * 64 + 16 * ((2 * kk + fh) ^ swz_c(fr)));
+        c_addr[0][kk] = lds0 + A_BYTES + (uint32_t)bro0 * 64 + off;
+        c_addr[1][kk] = lds0 + A_BYTES + (uint32_t)bro1 * 64 + off;
+    }
     const uint32_t s_addr0 = lds0 + OFF_S + (uint32_t)(bro0 + fr) * 16;
     const uint32_t s_addr1 = lds0 + OFF_S + (uint32_t)(bro1 + fr) * 16;
     uint32_t cm = 0x000F000Fu, cx = 0x43004300u;  // in VGPRs, so that and-or fuses
@@ -348,13 +359,13 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[mi][ni][i] = 0.f;
 
-    // ---- prologue: rows of item 0, then the first NS - 1 stages
+    // ---- prologue: rows of item 0, then the first stage
     fetch_rows(0);
     vm_wait_barrier<0>();
     setup_load(0);
-    issue(0, std::integral_constant<int, 0>{});
-    issue(1, std::integral_constant<int, 1>{});
-    issue(2, std::integral_constant<int, 2>{});
+    issue_scales(0);
+    for (int part = 0; part < 8; ++part) issue_part(part, std::integral_constant<int, 0>{});
+    advance();
 
     Item ci{};     // the compute cursor's item
     int xrow = 0;  // A row of tile row `lane` (the bias term's X splits)
@@ -371,13 +382,21 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
     auto step = [&](int gs, auto st_c) __attribute__((always_inline)) {
         constexpr int ST = decltype(st_c)::value;
         if (++ks == nks) ks = 0, ++cn;
-        const int younger = min(NS - 2, total_steps - 1 - gs);
-        if (younger >= 2) vm_wait_barrier<8>();
-        else if (younger == 1) vm_wait_barrier<4>();
-        else vm_wait_barrier<0>();
-        // this step's copies (NS - 1 steps ahead) are issued between its MFMAs
-        const bool copies = gs + NS - 1 < total_steps;
-        constexpr auto ST_L = std::integral_constant<int, (ST + NS - 1) % NS>{};
+        // K steps ST = 0, 1 read ring slot 0, ST = 2, 3 slot 1. A stage starts at even ST: its
+        // copies (issued during the previous stage) must have landed, and every wave must be done
+        // with the slot that the next stage's copies, issued between this K step's MFMAs, fill.
+        constexpr int SLOT = ST >> 1;
+        constexpr bool SS = (ST & 1) == 0;
+        // After the last stage the copies go on, in bounds (the load cursor stays on the last
+        // item), into the slot that is no longer read: the MFMA loop then has no branch.
+        if constexpr (SS) {
+            vm_wait_barrier<0>();
+            if (SLOT == 1 && (l_ks & 7) == 0 && gs + KS < total_steps) issue_scales(gs + KS);
+        }
+        constexpr auto SLOT_N = std::integral_constant<int, 1 - SLOT>{};
+        // the load cursor moves on at the start of the K step after the one that issued its copies
+        // (a branch right after the MFMA loop lets the compiler sink the loop's FMAs past it)
+        if constexpr (!SS) advance();
 
         if (ST == 0 && ks == 0) {
             ci = item_of(cn);
@@ -411,16 +430,16 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
         }
 
         // ---- the K step: fragments from LDS (stage ST: immediate offsets)
-        constexpr int SA = ST * STAGE, SC = ST * STAGE + A_BYTES;
+        constexpr int SA = SLOT * STAGE + (ST & 1) * A_STEP, SC = SLOT * STAGE;
         const uint32_t spar = ((gs >> 3) & 1) * S_BYTES;
         // Reads in the order they are needed; LDS reads complete in order, so a partial lgkmcnt
         // wait covers the oldest ones (scalar loads in flight only make such waits stricter).
-        u32x4 cw0 = ds_read16<SC>(c_addr0);
+        u32x4 cw0 = ds_read16<SC>(c_addr[0][ST & 1]);
         u32x4 a00 = ds_read16<SA>(a_off[0]), a10 = ds_read16<SA + 4096>(a_off[0]);
         u32x4 a01 = ds_read16<SA>(a_off[1]), a11 = ds_read16<SA + 4096>(a_off[1]);
         u32x4 a02 = ds_read16<SA>(a_off[2]), a12 = ds_read16<SA + 4096>(a_off[2]);
         u32x4 a03 = ds_read16<SA>(a_off[3]), a13 = ds_read16<SA + 4096>(a_off[3]);
-        u32x4 cw1 = ds_read16<SC>(c_addr1);
+        u32x4 cw1 = ds_read16<SC>(c_addr[1][ST & 1]);
         if (ST == 0) {  // the scales of this 8-step chunk: 8 groups per B row
             sch0 = ds_read16<0>(s_addr0 + spar);
             sch1 = ds_read16<0>(s_addr1 + spar);
@@ -456,7 +475,7 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
                                                         __builtin_bit_cast(mg_bf16x8, e),
                                                         s ? pt : z, 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
-            if ((q & 3) == 1 && copies) issue_part(gs + NS - 1, q >> 2, ST_L);
+            if (SS && (q & 1)) issue_part(q >> 1, SLOT_N);
             // 4 scale FMAs: slot q's share of pend (q < 8) or of fragment 0 (q >= 8)
             if (q == 8) {
                 if (ST == 0) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(sch0), "+v"(sch1));
@@ -484,7 +503,6 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
             __builtin_amdgcn_sched_barrier(0);
         }
         sc_pend = scale_of(sch1);
-        if (copies) advance(ST_L);
         if (c_now >= 0) {  // bias term of chunk c_now: X splits against b (lane half 0), -128 s (1)
             const uint32_t xo = lds0 + OFF_X + 16 * fr;
             u32x4 xa00 = ds_read16<0>(xo), xa01 = ds_read16<1024>(xo), xa02 = ds_read16<2048>(xo);
@@ -630,7 +648,7 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
     };
     // each K step is scheduled on its own (sched_barrier): interleaving neighbouring steps only
     // lengthens live ranges past the register budget of two waves per SIMD
-    for (int gs = 0; gs < total_steps; gs += NS) {
+    for (int gs = 0; gs < total_steps; gs += 4) {
         step(gs, std::integral_constant<int, 0>{});
         __builtin_amdgcn_sched_barrier(0);
         step(gs + 1, std::integral_constant<int, 1>{});
@@ -640,6 +658,7 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
         step(gs + 3, std::integral_constant<int, 3>{});
         __builtin_amdgcn_sched_barrier(0);
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the trailing copies
 }
 
 bool moe_gemm_supported(const MoeGemmJob &j) {
