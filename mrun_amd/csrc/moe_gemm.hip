@@ -51,11 +51,14 @@ constexpr int C_BYTES = BNR * 32 * KS;         // codes of a stage: 256 B rows x
 constexpr int STAGE = A_BYTES + C_BYTES;       // 32 KB
 constexpr int S_BYTES = BNR * 16;              // scales of 8 groups per B row
 constexpr int R_BYTES = BM * 4;                // A rows (tokens) of a routed tile
+constexpr int T_BYTES = 256;                   // a routed tile's record (copied as 64 dwords)
 constexpr int X_BYTES = BM * 3 * 16;           // bias term: X splits of 8 entries per row
 constexpr int B_BYTES = BNR * 16;              // bias term: biases of 8 groups per B row
-constexpr int OFF_S = NSTG * STAGE, OFF_R = OFF_S + 2 * S_BYTES, OFF_X = OFF_R + 3 * R_BYTES;
+constexpr int OFF_S = NSTG * STAGE, OFF_R = OFF_S + 2 * S_BYTES, OFF_T = OFF_R + 2 * R_BYTES;
+constexpr int OFF_X = OFF_T + 2 * T_BYTES;
 constexpr int OFF_B = OFF_X + X_BYTES;
-constexpr int LDS_BYTES = OFF_B + B_BYTES;     // 81,664: two workgroups per CU
+constexpr int LDS_BYTES = OFF_B + B_BYTES;     // 81,920: two workgroups per CU
+static_assert(LDS_BYTES <= 81920, "two workgroups per CU");
 }  // namespace mg
 
 __device__ __forceinline__ uint32_t lds_offset(const void *p) {
@@ -82,8 +85,8 @@ __device__ __forceinline__ uint32_t ds_read2(uint32_t a) {
 // that no per-lane 64-bit address arithmetic is needed. 16 (or 4) bytes per lane land at
 // lds + 16 * lane (4 * lane); the LDS address is the same for the whole wave.
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
-__device__ __forceinline__ rsrc_t rsrc_of(const void *p) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, (int)0xFFFFFFFFu, 0x00020000);
+__device__ __forceinline__ rsrc_t rsrc_of(const void *p, uint32_t bytes = 0xFFFFFFFFu) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, (int)bytes, 0x00020000);
 }
 __device__ __forceinline__ void dma16(rsrc_t r, uint32_t voff, uint32_t soff, char *lds) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)lds, 16, voff, soff, 0, 0);
@@ -183,19 +186,6 @@ __device__ __forceinline__ const T *unip(const T *p) {
     return (const T *)(uintptr_t)(((uint64_t)hi << 32) | lo);
 }
 
-// A routed tile's record (expert, first row, rows) through the scalar cache. The tile list is
-// written by an earlier launch and only read by this one; a plain load would go through the
-// vector memory counter, whose waits would also wait for the global-to-LDS copies in flight.
-__device__ __forceinline__ void tile_record(const uint32_t *t3, int &e, int &row0, int &mrows) {
-    uint64_t ab;
-    uint32_t c;
-    asm volatile("s_load_dwordx2 %0, %2, 0x0\n\ts_load_dword %1, %2, 0x8\n\ts_waitcnt lgkmcnt(0)"
-                 : "=s"(ab), "=s"(c)
-                 : "s"(t3)
-                 : "memory");
-    e = (int)(uint32_t)ab, row0 = (int)(uint32_t)(ab >> 32), mrows = (int)c;
-}
-
 // LDS swizzles (16-byte units). A rows are 128 B (8 units): rows r and r + 8 (same bank window
 // at 256 B per cycle) and rows of one parity in 16 get distinct masks. B rows are 64 B (4 units,
 // two K steps of codes): the 4 rows of a 256-byte window... rows r, r + 4, r + 8, r + 12 (which
@@ -232,9 +222,17 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
         int e, row0, mrows, n0, tile;  // tile: routed tile index (rows from the table), or -1
         bool sh;
     };
-    auto item_of = [&](int n) __attribute__((always_inline)) {
+    // item n's row tile (shared tiles first) and column block
+    auto item_pos = [&](int n, int &rt, int &cb) __attribute__((always_inline)) {
         const int i = seg_lo + slot + G8 * n;
-        const int rt = uni(i / NB), cb = i - rt * NB;
+        rt = uni(i / NB), cb = i - rt * NB;
+    };
+    // A routed tile's record (expert, first row, rows) and token rows reach LDS through copies
+    // that wave 0 issues one item ahead (fetch_rows), into slot n % 2: no scalar-cache miss and
+    // no wait on a global load at an item switch.
+    auto item_of = [&](int n) __attribute__((always_inline)) {
+        int rt, cb;
+        item_pos(n, rt, cb);
         Item it;
         it.n0 = cb * NCOLS;
         if (rt < s_tiles) {
@@ -244,7 +242,10 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
             it.sh = false;
             const int r = rt - s_tiles;
             if (j.has_routing) {
-                tile_record(j.routing.tiles + 3 * (size_t)r, it.e, it.row0, it.mrows);
+                const uint32_t rec = lds0 + OFF_T + (uint32_t)(n & 1) * T_BYTES;
+                uint32_t e = ds_read4(rec), row0 = ds_read4(rec + 4), mrows = ds_read4(rec + 8);
+                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(e), "+v"(row0), "+v"(mrows));
+                it.e = uni((int)e), it.row0 = uni((int)row0), it.mrows = uni((int)mrows);
                 it.tile = j.tile_rows ? r : -1;
             } else {
                 it.e = 0, it.row0 = r * BM, it.mrows = min(BM, j.M - it.row0), it.tile = -1;
@@ -266,25 +267,33 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
     rsrc_t r_a, r_c0, r_c1, r_s;
     uint32_t la0 = 0, la1 = 0, lc[4] = {0u, 0u, 0u, 0u}, ls = 0;
     int l_item = 0, l_ks = 0;
+    Item li{};     // the load cursor's item, taken over by the compute cursor at its switch
+    int lx = 0;    // the load cursor's A row of tile row `lane` (the bias term's X splits)
 
     // the A row (token) of tile row r of item n
     auto a_row = [&](const Item &it, int n, int r) __attribute__((always_inline)) -> int {
         const int rr = min(r, it.mrows - 1);
-        if (it.tile >= 0) return (int)ds_read4(lds0 + OFF_R + (n % 3) * R_BYTES + 4 * rr);
+        if (it.tile >= 0) return (int)ds_read4(lds0 + OFF_R + (n & 1) * R_BYTES + 4 * rr);
         return it.row0 + rr;
     };
-    // copy the token rows of item n's routed tile into its row buffer (wave 0)
+    // copy item n's tile record and token rows into LDS slot n % 2 (wave 0; routed tiles)
     auto fetch_rows = [&](int n) __attribute__((always_inline)) {
-        if (n >= n_items || wave != 0) return;
-        const Item it = item_of(n);
-        if (it.tile < 0) return;
-        dma4(rsrc_of(j.tile_rows), 4u * (uint32_t)lane, 4u * (uint32_t)(it.tile * BM),
-             rowbuf + (n % 3) * R_BYTES);
+        if (n >= n_items || wave != 0 || !j.has_routing) return;
+        int rt, cb;
+        item_pos(n, rt, cb);
+        if (rt < s_tiles) return;
+        const int r = rt - s_tiles;
+        dma4(rsrc_of(j.routing.tiles, 12u * (uint32_t)j.max_tiles), 4u * (uint32_t)lane,
+             12u * (uint32_t)r, smem + OFF_T + (n & 1) * T_BYTES);
+        if (j.tile_rows)
+            dma4(rsrc_of(j.tile_rows), 4u * (uint32_t)lane, 4u * (uint32_t)(r * BM),
+                 rowbuf + (n & 1) * R_BYTES);
     };
     auto setup_load = [&](int n) __attribute__((always_inline)) {
         const Item it = item_of(n);
-        int r0 = a_row(it, n, ra), r1 = a_row(it, n, ra + 32);
-        if (it.tile >= 0) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r0), "+v"(r1));
+        int r0 = a_row(it, n, ra), r1 = a_row(it, n, ra + 32), x0 = a_row(it, n, lane);
+        if (it.tile >= 0) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r0), "+v"(r1), "+v"(x0));
+        li = it, lx = x0;
         const int lda = it.sh ? j.sh.lda : j.lda;
         r_a = rsrc_of(it.sh ? j.sh.A : j.A);
         la0 = (uint32_t)r0 * (uint32_t)lda * 2u + ua16;
@@ -398,11 +407,8 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
         // (a branch right after the MFMA loop lets the compiler sink the loop's FMAs past it)
         if constexpr (!SS) advance();
 
-        if (ST == 0 && ks == 0) {
-            ci = item_of(cn);
-            int x0 = a_row(ci, cn, lane);
-            if (ci.tile >= 0) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x0));
-            xrow = x0;
+        if (ST == 0 && ks == 0) {  // the load cursor is on this item (it is at least 4 K steps long)
+            ci = li, xrow = lx;
             no_bias = ci.sh ? j.sh.w0.biases == nullptr : j.w0.biases == nullptr;
         }
         // the bias term: chunk c (entries 8c .. 8c + 7, i.e. groups 8c / H .. of this item) runs
