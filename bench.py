@@ -139,10 +139,11 @@ def time_stages(dev, x, reps: int, torch):
     return {name: float(acc[i] / reps * 1e3) for i, name in enumerate(names)}  # microseconds
 
 
-def time_gateup_kernel(dev, x, reps: int, torch) -> float:
+def time_gateup_kernel(dev, x, reps: int, torch, cold=None) -> float:
     """Mean duration of the decode gate/up kernel in microseconds: events updated by its own launch
     at the kernel's start and end (mrun_moe_forward_timed, hipExtLaunchKernel), one pair per
-    forward, on the launch stream; no launch gap is included."""
+    forward, on the launch stream; no launch gap is included. With `cold` (a ColdTimer) the
+    last-level cache is flushed before every forward (outside the kernel's events)."""
     from mrun_amd import _lib
     lib = _lib.load()
     T = x.shape[0]
@@ -151,6 +152,8 @@ def time_gateup_kernel(dev, x, reps: int, torch) -> float:
     out = torch.empty_like(x)
     ws = dev.workspace(T)
     for r in range(reps):
+        if cold is not None:
+            cold.flush(stream)
         _lib.check(lib.mrun_moe_forward_timed(
             ctypes.byref(dev.c), ctypes.c_void_p(x.data_ptr()), T, ctypes.c_void_p(out.data_ptr()),
             ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(stream.cuda_stream),
@@ -159,8 +162,10 @@ def time_gateup_kernel(dev, x, reps: int, torch) -> float:
     return float(np.mean([ev.ms(2 * r, 2 * r + 1) for r in range(1, reps)]) * 1e3)
 
 
-def time_graph(dev, x, steps: int, torch):
-    """Replay time of the forward captured in a HIP graph (launch overhead amortised)."""
+def time_graph(dev, x, steps: int, torch, per_graph: int = 1):
+    """Device time per forward of `per_graph` forwards captured in one HIP graph, replayed
+    back to back. With one forward per graph the replays are bound by the host's graph launch
+    (hipGraphLaunch takes longer than the three kernels); per_graph > 1 amortises it."""
     out = torch.empty_like(x)
     ws = dev.workspace(x.shape[0])
     s = torch.cuda.Stream()
@@ -172,51 +177,117 @@ def time_graph(dev, x, steps: int, torch):
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
-        dev.forward(x, out=out, workspace=ws, stream=s)
+        for _ in range(per_graph):
+            dev.forward(x, out=out, workspace=ws, stream=s)
     torch.cuda.synchronize()
     for _ in range(3):
         g.replay()
     ev = Events(2)
     stream = torch.cuda.current_stream()
+    reps = max(steps // per_graph, 3)
     torch.cuda.synchronize()
     ev.record(0, stream)
-    for _ in range(steps):
+    for _ in range(reps):
         g.replay()
     ev.record(1, stream)
     torch.cuda.synchronize()
-    return ev.ms(0, 1) / steps, out
+    return ev.ms(0, 1) / (reps * per_graph), out
 
 
-def cpu_baseline(hb, x_np, seconds: float, seconds_1t: float = 4.0):
-    """The CPU restatement on this host's cores, repeated for about `seconds` after one warm-up
-    forward (the median forward is reported), then on one thread for about `seconds_1t`."""
+def _cpu_run(fn, budget: float, min_reps: int = 3, max_reps: int = 2000):
+    """Median seconds of fn() repeated for about `budget` seconds after one warm-up call."""
+    fn()
+    times, t0 = [], time.perf_counter()
+    while True:
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+        el = time.perf_counter() - t0
+        if (el >= budget and len(times) >= min_reps) or len(times) >= max_reps:
+            break
+    return float(np.median(times)), len(times), el
+
+
+def cpu_baseline(args, Q, synth, hb, x_np) -> dict:
+    """The CPU restatement (oracle/, scalar C with OpenMP over pairs and rows) on this host's
+    cores: the headline configs[1] T = 1 point (all cores, then one thread) and one entry per
+    config in `per_config`. Large points time a sample of token rows (rows are independent) or
+    2 of the 40 stack layers, as each entry's `sample` says."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import oracle as O
     cores = len(os.sched_getaffinity(0))
+    threads = O.set_threads(cores)
+    sec = args.cpu_seconds
+    where = (f"OpenMP over {threads} threads (sched_getaffinity {cores}, hardware "
+             f"{os.cpu_count()})")
 
-    def run(threads, budget):
-        used = O.set_threads(threads)
-        O.moe_forward(hb, x_np)  # warm
-        times, t0 = [], time.perf_counter()
-        while True:
-            t = time.perf_counter()
-            O.moe_forward(hb, x_np)
-            times.append(time.perf_counter() - t)
-            if (time.perf_counter() - t0 >= budget and len(times) >= 5) or len(times) >= 2000:
-                break
-        return used, float(np.median(times)), len(times), time.perf_counter() - t0
+    def entry(tokens: int, med: float, sample: str) -> dict:
+        return {"value": tokens / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+                "sample": f"{sample}; {where}; median s/forward {med:.4g}"}
 
-    threads, med, reps, el = run(cores, seconds)
-    _, med1, reps1, el1 = run(1, seconds_1t)
-    O.set_threads(cores)
+    def block_point(blk, x, label: str, budget: float, min_reps: int = 3) -> dict:
+        med, reps, el = _cpu_run(lambda: O.moe_forward(blk, x), budget, min_reps)
+        return entry(x.shape[0], med, f"{reps} block forwards at T={x.shape[0]} ({el:.1f} s), "
+                                      f"{label}")
+
+    per = {}
+    print("[bench] CPU baseline configs[1]", file=sys.stderr, flush=True)
     T = x_np.shape[0]
-    return {"value": T / med, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{reps} block forwards at T={T} ({el:.1f} s), same seeded block, OpenMP "
-                      f"over {threads} threads (sched_getaffinity {cores}, hardware "
-                      f"{os.cpu_count()}); median us/block {med * 1e6:.0f}",
-            "one_thread": {"value": T / med1, "unit": "tokens/s", "cores": 1,
-                           "sample": f"{reps1} block forwards ({el1:.1f} s); median us/block "
-                                     f"{med1 * 1e6:.0f}"}}
+    med, reps, el = _cpu_run(lambda: O.moe_forward(hb, x_np), sec, 5)
+    head = entry(T, med, f"{reps} block forwards at T={T} ({el:.1f} s), the seeded configs[1] block")
+    O.set_threads(1)
+    med1, reps1, el1 = _cpu_run(lambda: O.moe_forward(hb, x_np), sec / 3, 3)
+    O.set_threads(cores)
+    head["one_thread"] = {"value": T / med1, "unit": "tokens/s", "cores": 1,
+                          "sample": f"{reps1} block forwards ({el1:.1f} s); median s/forward "
+                                    f"{med1:.4g}"}
+    per[f"configs[1] T={T}"] = {k: v for k, v in head.items() if k != "one_thread"}
+    for t in (1, 2, 4, 16):
+        if t != T:
+            per[f"configs[1] T={t}"] = block_point(
+                hb, synth.make_x(Q, t, config=synth.CFG_DECODE, layer=t), "configs[1] block", 2.0)
+    print("[bench] CPU baseline configs[0], configs[2]", file=sys.stderr, flush=True)
+    h0 = synth.make_block(Q, config=synth.CFG_PLUMBING)
+    per["configs[0] T=16"] = block_point(h0, synth.make_x(Q, 16, config=synth.CFG_PLUMBING),
+                                         "configs[0] plumbing block", 2.0)
+    del h0
+    hz = synth.make_block(Q, config=synth.CFG_PREFILL_ZIPF, zipf=True)
+    xz = synth.make_x(Q, 2048, config=synth.CFG_PREFILL_ZIPF)[:256]
+    pz = block_point(hz, xz, "the first 256 of the 2,048 token rows of the configs[2] input "
+                             "(Zipf router; each expert row is dequantised once per forward, so "
+                             "fewer rows understate the full-batch rate)", 1.0, 1)
+    per["configs[2] T=2048"] = pz
+    del hz
+    print("[bench] CPU baseline configs[3]", file=sys.stderr, flush=True)
+    layers = [synth.make_block(Q, config=synth.CFG_STACK, layer=l) for l in range(2)]
+    for t, rows in ((1, 1), (4096, 32)):
+        xs = synth.make_x(Q, t, config=synth.CFG_STACK, layer=t)[:rows]
+        med, reps, el = _cpu_run(lambda: O.moe_stack(layers, xs, None, 1e-6), 2.0, 1)
+        per_layer = med / 2
+        per[f"configs[3] T={t}"] = {
+            "value": rows / (40 * per_layer), "unit": "tokens/s (40-layer pass)",
+            "cores": threads, "kind": "port",
+            "sample": f"{reps} passes of {rows} token row(s) through 2 of the 40 seeded layers "
+                      f"(pre-RMSNorm and residual add each) ({el:.1f} s), scaled to 40 layers; "
+                      f"{where}; median s/layer {per_layer:.4g}"}
+    del layers
+    if not args.no_coder:
+        print("[bench] CPU baseline configs[4] (generating the block on the host)",
+              file=sys.stderr, flush=True)
+        C = synth.CODER
+        hc = synth.make_block(C, config=synth.CFG_CODER)
+        for t in (1, 8):
+            per[f"configs[4] T={t}"] = block_point(
+                hc, synth.make_x(C, t, config=synth.CFG_CODER, layer=t), "configs[4] Coder block",
+                2.0, 1)
+        xc = synth.make_x(C, 8192, config=synth.CFG_CODER, layer=8192)[:16]
+        per["configs[4] T=8192"] = block_point(
+            hc, xc, "the first 16 of the 8,192 token rows of the configs[4] prefill input (each "
+                    "expert row is dequantised once per forward, so fewer rows understate the "
+                    "full-batch rate)", 1.0, 1)
+        del hc
+    head["per_config"] = per
+    return head
 
 
 def calib_lib():
@@ -241,16 +312,18 @@ class ColdTimer:
         self.rout = torch.empty(self.lib.mrun_calib_read_threads(), dtype=torch.int32,
                                 device="cuda")
 
+    def flush(self, stream) -> None:
+        assert self.lib.mrun_calib_read(self.buf.data_ptr(), 1 << 30, self.rout.data_ptr(),
+                                        ctypes.c_void_p(stream.cuda_stream)) == 0
+
     def time(self, dev, x, n: int) -> float:
         stream = self.torch.cuda.current_stream()
-        sp = ctypes.c_void_p(stream.cuda_stream)
         out = self.torch.empty_like(x)
         ws = dev.workspace(x.shape[0])
         ev = Events(2)
         tot = 0.0
         for _ in range(n):
-            assert self.lib.mrun_calib_read(self.buf.data_ptr(), 1 << 30, self.rout.data_ptr(),
-                                            sp) == 0
+            self.flush(stream)
             ev.record(0, stream)
             dev.forward(x, out=out, workspace=ws)
             ev.record(1, stream)
@@ -328,10 +401,12 @@ def prefill_point(args, Q, M, synth, torch) -> dict:
     return {"tokens": T, "ms_per_step": wall, "device_ms": dev_ms,
             "tokens_per_s": T / (wall * 1e-3), "us_per_layer": dev_ms * 1e3,
             "stages_us": stages, "flops": fl,
-            "block_mfma_frac": fl["block"] / (dev_ms * 1e-3) / MFMA_BF16_PEAK,
-            "gate_up_mfma_frac": (fl["gate_up"] + fl["shared"] * 2 / 3)
+            "cache": "warm: repeated forwards (the block's 402 MB of expert weights exceed the "
+                     "256 MB last-level cache, so most of them come from HBM anyway)",
+            "block_mfma_frac_warm": fl["block"] / (dev_ms * 1e-3) / MFMA_BF16_PEAK,
+            "gate_up_mfma_frac_warm": (fl["gate_up"] + fl["shared"] * 2 / 3)
             / (stages["gate_up"] * 1e-6) / MFMA_BF16_PEAK,
-            "down_mfma_frac": (fl["down"] + fl["shared"] / 3)
+            "down_mfma_frac_warm": (fl["down"] + fl["shared"] / 3)
             / (stages["down"] * 1e-6) / MFMA_BF16_PEAK}
 
 
@@ -393,10 +468,11 @@ def stack_point(args, Q, M, synth, torch) -> dict:
         if T == 1:
             # one token picks top_k distinct experts in every layer; plus the norm's x, h traffic
             b = n * (decode_bytes(Q, Q.top_k, 1)["block"] + 4 * Q.hidden)
-            pt.update(bytes=b, hbm_frac=b / (dev_ms * 1e-3) / HBM_PEAK)
+            # 18 GB of weights, 70x the last-level cache: every layer reads them from HBM
+            pt.update(bytes=b, hbm_frac_cold=b / (dev_ms * 1e-3) / HBM_PEAK)
         else:
             f = n * prefill_flops(Q, T)["block"]
-            pt.update(flops=f, mfma_frac=f / (dev_ms * 1e-3) / MFMA_BF16_PEAK)
+            pt.update(flops=f, mfma_frac_cold=f / (dev_ms * 1e-3) / MFMA_BF16_PEAK)
         out[f"T{T}"] = pt
         del x, x0
     del st, layers
@@ -404,7 +480,7 @@ def stack_point(args, Q, M, synth, torch) -> dict:
     return out
 
 
-def coder_point(args, M, synth, torch) -> dict:
+def coder_point(args, M, synth, torch, cold=None) -> dict:
     """the Coder-shaped block (hidden 6144, 160 experts, top-8, FFN 2560, no shared
     expert; 4.2 GB of 4-bit weights, generated on the device) at decode T = 1 and 8, where a block
     streams 8 experts' 26.5 MB each, and at prefill T = 8192."""
@@ -425,10 +501,16 @@ def coder_point(args, M, synth, torch) -> dict:
             _, _, ids, _ = dev.router_forward(x)
             n_active = int(np.unique(M.u32_array(ids)).size)
             b = decode_bytes(C, n_active, T)["block"]
-            pt.update(n_active=n_active, bytes=b, hbm_frac=b / (dev_ms * 1e-3) / HBM_PEAK)
+            # warm: the repeated forward reads the same experts' 212 MB (T = 1), which the 256 MB
+            # last-level cache holds; cold: that cache flushed before every forward
+            pt.update(n_active=n_active, bytes=b, hbm_frac_warm=b / (dev_ms * 1e-3) / HBM_PEAK)
+            if cold is not None:
+                cms = cold.time(dev, x, 10)
+                pt.update(cold_device_ms=cms, hbm_frac_cold=b / (cms * 1e-3) / HBM_PEAK)
         else:
             f = prefill_flops(C, T)["block"]
-            pt.update(flops=f, mfma_frac=f / (dev_ms * 1e-3) / MFMA_BF16_PEAK)
+            # 4.2 GB of weights, read by every forward: past the last-level cache
+            pt.update(flops=f, mfma_frac_cold=f / (dev_ms * 1e-3) / MFMA_BF16_PEAK)
         out[f"T{T}"] = pt
         del x
     del dev
@@ -454,7 +536,7 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--tokens", type=int, default=1)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=6.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
@@ -518,28 +600,39 @@ def main(argv=None) -> int:
         stages = time_stages(dev, x, 50, torch)
         try:
             g_ms, _ = time_graph(dev, x, steps, torch)
+            g16_ms, _ = time_graph(dev, x, steps, torch, per_graph=16)
         except Exception as e:  # graph capture is reported, never required
             print(f"[bench] graph capture failed: {e}", file=sys.stderr)
-            g_ms = None
+            g_ms = g16_ms = None
         b = decode_bytes(Q, n_active, T)
         return {"tokens": T, "n_active": n_active, "ms_per_step": wall, "device_ms": dev_ms,
-                "cold_device_ms": cold_ms, "graph_ms": g_ms, "tokens_per_s": T / (wall * 1e-3),
-                "stages_us": stages, "bytes": b,
-                "block_hbm_frac": b["block"] / (dev_ms * 1e-3) / HBM_PEAK}, x_np
+                "cold_device_ms": cold_ms, "graph_ms": g_ms, "graph16_ms": g16_ms,
+                "tokens_per_s": T / (wall * 1e-3), "stages_us": stages, "bytes": b,
+                "block_hbm_frac_warm": b["block"] / (dev_ms * 1e-3) / HBM_PEAK,
+                "block_hbm_frac_cold": (b["block"] / (cold_ms * 1e-3) / HBM_PEAK
+                                        if cold_ms else None)}, x_np
 
     print(f"[bench] decode T={args.tokens}", file=sys.stderr, flush=True)
     main_pt, x_main = decode_point(args.tokens, args.steps, args.warmup)
     gu_stage_us = main_pt["stages_us"]["gate_up"]
     gu_us = time_gateup_kernel(dev, M.bf16_tensor(x_main), 100, torch)
-    achieved = main_pt["bytes"]["gate_up"] / (gu_us * 1e-6)
+    gu_us_cold = (time_gateup_kernel(dev, M.bf16_tensor(x_main), 30, torch, cold=cold)
+                  if cold else None)
+    gbytes = main_pt["bytes"]["gate_up"]
+    achieved = gbytes / (gu_us * 1e-6)
     kname = "decode_gateup_kernel"
     roofline = {"kernel": f"{kname} (routed + shared gate/up, SwiGLU fused)", "bound": "hbm",
                 "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                 "frac": achieved / HBM_PEAK, "traffic": measured_traffic(kname),
-                "bytes_per_launch": main_pt["bytes"]["gate_up"], "us_per_launch": gu_us,
-                "us_per_launch_with_gap": gu_stage_us,
+                "cache": "frac is warm: the repeated forward keeps the 17 MB block in the 256 MB "
+                         "last-level cache; frac_cold: that cache flushed (a 1 GiB read) before "
+                         "every forward, outside the kernel's events",
+                "achieved_cold": gbytes / (gu_us_cold * 1e-6) / 1e9 if gu_us_cold else None,
+                "frac_cold": gbytes / (gu_us_cold * 1e-6) / HBM_PEAK if gu_us_cold else None,
+                "bytes_per_launch": gbytes, "us_per_launch": gu_us,
+                "us_per_launch_cold": gu_us_cold, "us_per_launch_with_gap": gu_stage_us,
                 "timing": "HIP events recorded by the launch itself at the kernel's start and end "
-                          "(hipExtLaunchKernel) on its stream, mean of 99 forwards; "
+                          "(hipExtLaunchKernel) on its stream, mean of 99 forwards (29 cold); "
                           "us_per_launch_with_gap: events between launches"}
 
     sweep = []
@@ -553,7 +646,7 @@ def main(argv=None) -> int:
 
     prefill = None if args.no_prefill else prefill_point(args, Q, M, synth, torch)
     stack = None if args.no_stack else stack_point(args, Q, M, synth, torch)
-    coder = None if args.no_coder else coder_point(args, M, synth, torch)
+    coder = None if args.no_coder else coder_point(args, M, synth, torch, cold)
 
     machine = None
     if not args.no_machine:
@@ -563,7 +656,7 @@ def main(argv=None) -> int:
     cpu = None
     if not args.no_cpu:
         print("[bench] CPU restatement baseline", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(hb, x_main, args.cpu_seconds)
+        cpu = cpu_baseline(args, Q, synth, hb, x_main)
 
     line = {
         "metric": "MoE block tokens/s + % HBM/MFMA roofline, decode T=1..16, prefill T=2048",
@@ -587,7 +680,9 @@ def main(argv=None) -> int:
         "cold_us_per_layer": (main_pt["cold_device_ms"] * 1e3 if main_pt["cold_device_ms"]
                               else None),
         "graph_us_per_layer": main_pt["graph_ms"] * 1e3 if main_pt["graph_ms"] else None,
-        "block_hbm_frac": main_pt["block_hbm_frac"],
+        "graph16_us_per_layer": main_pt["graph16_ms"] * 1e3 if main_pt["graph16_ms"] else None,
+        "block_hbm_frac_warm": main_pt["block_hbm_frac_warm"],
+        "block_hbm_frac_cold": main_pt["block_hbm_frac_cold"],
         "stages_us": main_pt["stages_us"],
         "roofline": roofline,
         "cpu_baseline": cpu,
