@@ -395,7 +395,8 @@ def prefill_point(args, Q, M, synth, torch) -> dict:
     dz = M.SparseMoe(hz)
     T = 2048
     xz = M.bf16_tensor(synth.make_x(Q, T, config=synth.CFG_PREFILL_ZIPF))
-    wall, dev_ms, _ = time_forward(dz, xz, max(args.steps // 10, 10), 3, torch)
+    # 30 warm-up forwards: the first few milliseconds of back-to-back prefill run at lower clocks
+    wall, dev_ms, _ = time_forward(dz, xz, max(args.steps // 4, 20), 30, torch)
     stages = time_stages(dz, xz, 10, torch)
     fl = prefill_flops(Q, T)
     return {"tokens": T, "ms_per_step": wall, "device_ms": dev_ms,

@@ -186,11 +186,11 @@ constexpr int kGemmTileN = 64;
 
 // The prefill forward's grouped expert GEMM (moe_gemm.hip): 4-bit group-64 weights (biases may be
 // null), K % 512 == 0, N a multiple of 128 (glu) or 256. A is packed (launch_apack) with its X
-// splits AX [rows][3][ax_e] (ax_e = K / 64, or 2 K / 64 for two half-group sums per group).
+// splits AX [rows][3][ax_e] (ax_e = K / 64: one entry per group).
 // Routed tiles come from routing.tiles (64 rows); their A rows from tile_rows [tile][64] (token
 // of each tile row, the tile's last row repeated past its rows) or, without tile_rows, the sorted
-// positions themselves. glu: out = packed R(silu(R(A.w0)) * R(A.w1)) and OX [rows][3][2 N / 64]
-// the X splits of each output row's half groups; else out = R(A.w0). The shared product (sh)
+// positions themselves. glu: out = packed R(silu(R(A.w0)) * R(A.w1)) and OX [rows][3][N / 64]
+// the X splits of each output row's groups; else out = R(A.w0). The shared product (sh)
 // has the same K and N and comes first.
 struct MoeGemmJob {
     const bf16_t *A;

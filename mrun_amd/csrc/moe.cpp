@@ -207,13 +207,13 @@ static Plan make_plan(const mrun_moe_config &c, int T) {
         p.sh_act = take(2 * (size_t)T * S);
         p.sh_y = take(2 * (size_t)T * D);
     }
-    // prefill GEMM operands (moe_gemm.hip): packed x and its group-sum splits, the half-group
+    // prefill GEMM operands (moe_gemm.hip): packed x and its group-sum splits, the group-sum
     // splits of act (and of the shared expert's act), the token rows of each routed tile
     if (T > 16) {
         p.xp = take(2 * (size_t)T * D);
         p.xs = take(2 * 3 * (size_t)T * (D / 64));
-        p.act_x = take(2 * 3 * P * (2 * (I / 64)));
-        if (S > 0) p.sh_act_x = take(2 * 3 * (size_t)T * (2 * (S / 64)));
+        p.act_x = take(2 * 3 * P * (I / 64));
+        if (S > 0) p.sh_act_x = take(2 * 3 * (size_t)T * (S / 64));
         p.tile_rows = take(4 * (size_t)p.max_tiles * kGemmTileM);
     }
     p.total = at;
@@ -452,7 +452,7 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
         mg.w0 = qw_of(m.switch_gate_proj), mg.w1 = qw_of(m.switch_up_proj);
         mg.routing = rt, mg.has_routing = 1, mg.max_tiles = p.max_tiles;
         mg.out = act, mg.ldo = I, mg.OX = (bf16_t *)at(p.act_x);
-        md.A = act, md.lda = I, md.AX = (const bf16_t *)at(p.act_x), md.ax_e = 2 * (I / 64);
+        md.A = act, md.lda = I, md.AX = (const bf16_t *)at(p.act_x), md.ax_e = I / 64;
         md.K = I, md.N = D, md.glu = 0, md.w0 = qw_of(m.switch_down_proj);
         md.routing = rt, md.has_routing = 1, md.max_tiles = p.max_tiles, md.out = y, md.ldo = D;
         new_path = moe_gemm_supported(mg) && moe_gemm_supported(md);
@@ -462,7 +462,7 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
             tg.sh = {mg.A, D, mg.AX, D / 64, T, qw_of(m.shared_gate_proj.q),
                      qw_of(m.shared_up_proj.q), sh_act, S, (bf16_t *)at(p.sh_act_x)};
             tg.has_shared = 1;
-            td.sh = {sh_act, S, (const bf16_t *)at(p.sh_act_x), 2 * (S / 64), T,
+            td.sh = {sh_act, S, (const bf16_t *)at(p.sh_act_x), S / 64, T,
                      qw_of(m.shared_down_proj.q), QW{}, sh_y, D, nullptr};
             td.has_shared = 1;
             if (moe_gemm_supported(tg) && moe_gemm_supported(td)) mg = tg, md = td, fuse_new = true;

@@ -12,10 +12,9 @@
 //    order the MFMA fragments read them (block 4h + s at position 2s + h: K sub-step s, lane half
 //    h) and each block is re-paired (x0, x4, x1, x5, x2, x6, x3, x7) to match the code expansion
 //    (dword i of an expanded word holds codes i and i + 4). The GEMM copies A into LDS unchanged.
-//  - X is stored split exactly into three bf16 (hi + mid + lo == X, truncation) per entry:
-//    XS [rows][3][entries]. apack_kernel writes one entry per group of x; the gate/up epilogue
-//    writes two per group of act (each workgroup wave covers half of a 64-column group), and the
-//    bias term sums both.
+//  - X is stored split exactly into three bf16 (hi + mid + lo == X, truncation) per group:
+//    XS [rows][3][K / 64]. apack_kernel writes those of x; the gate/up epilogue those of act (the
+//    two waves covering a 64-column group add their half sums, handed over through LDS).
 //  - The bias term  sum_g X_g (b_g - 128 s_g)  is a small MFMA product per tile: K entries of
 //    X splits against b (lane half 0) and -128 s (lane half 1; exact), 3 MFMAs per 8 entries.
 //
@@ -388,6 +387,37 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) part0[mi][i] = part1[mi][i] = 0.f;
 
+    // The gate/up epilogue's group sums of act: the odd wave of each pair writes its half sums to
+    // LDS after the next stage's barrier (every wave is then done with the bias operands there),
+    // the even wave adds them to its own after the barrier that follows and stores the splits.
+    // x_state: 0 nothing pending, 1 the write, 2 the read.
+    int x_state = 0;
+    float x_pend = 0.f;
+    bf16_t *x_dst = nullptr;  // this lane's row entry, or null past the tile's rows
+    const int x_oxe = j.N / 64;
+    const uint32_t x_slot = lds0 + OFF_X + 256u * (uint32_t)(wave >> 1) + 4u * (uint32_t)lane;
+    auto x_write = [&]() __attribute__((always_inline)) {
+        if (wave & 1) {
+            asm volatile("ds_write_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" ::"v"(x_slot), "v"(x_pend)
+                         : "memory");
+        }
+        x_state = 2;
+    };
+    auto x_read_store = [&]() __attribute__((always_inline)) {
+        if (!(wave & 1)) {
+            uint32_t o = ds_read4(x_slot);
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(o));
+            if (x_dst) {
+                uint32_t hi, mid, lo;
+                split3(x_pend + __uint_as_float(o), hi, mid, lo);
+                x_dst[0] = (bf16_t)hi;
+                x_dst[x_oxe] = (bf16_t)mid;
+                x_dst[2 * x_oxe] = (bf16_t)lo;
+            }
+        }
+        x_state = 0;
+    };
+
     auto step = [&](int gs, auto st_c) __attribute__((always_inline)) {
         constexpr int ST = decltype(st_c)::value;
         if (++ks == nks) ks = 0, ++cn;
@@ -401,6 +431,10 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
         if constexpr (SS) {
             vm_wait_barrier<0>();
             if (SLOT == 1 && (l_ks & 7) == 0 && gs + KS < total_steps) issue_scales(gs + KS);
+            if constexpr (GLU) {
+                if (ST == 0 && x_state == 1) x_write();
+                else if (ST == 2 && x_state == 2) x_read_store();
+            }
         }
         constexpr auto SLOT_N = std::integral_constant<int, 1 - SLOT>{};
         // the load cursor moves on at the start of the K step after the one that issued its copies
@@ -411,11 +445,10 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
             ci = li, xrow = lx;
             no_bias = ci.sh ? j.sh.w0.biases == nullptr : j.w0.biases == nullptr;
         }
-        // the bias term: chunk c (entries 8c .. 8c + 7, i.e. groups 8c / H .. of this item) runs
-        // at the last K step of its groups, per (c + 1) - 1, and loads its operands 3 steps before
-        constexpr int H = GLU ? 1 : 2;  // entries per group: 1 (x) or 2 (act: two half-group sums)
-        constexpr int per = 8 / H;       // K steps per chunk: 8 or 4
-        const int axe = H * G;
+        // the bias term: chunk c (groups 8c .. 8c + 7 of this item) runs at the last K step of its
+        // groups, 8 (c + 1) - 1, and loads its operands 3 steps before
+        constexpr int per = 8;  // K steps per chunk
+        const int axe = G;
         const int c_now = (ks + 1) % per == 0 ? (ks + 1) / per - 1 : -1;
         const int c_pre = ST == 0 && (ks + 4) % per == 0 ? (ks + 4) / per - 1 : -1;
         if (c_pre >= 0) {  // the chunk's X splits (waves 0-2) and biases into LDS
@@ -429,9 +462,9 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
                 const uint32_t wrow = (uint32_t)ci.e * (uint32_t)(ci.sh ? j.sh.w0.out : j.w0.out) + col;
                 const bf16_t *bg = ci.sh ? j.sh.w0.biases : j.w0.biases;
                 const bf16_t *bu = GLU ? (ci.sh ? j.sh.w1.biases : j.w1.biases) : bg;
-                // the 16-byte aligned 8 groups holding the chunk's groups (H = 2: two chunks)
-                dma16(rsrc_of(upr ? bu : bg), 2u * wrow * (uint32_t)G,
-                      2u * (uint32_t)(((8 * c_pre) / H) & ~7), smem + OFF_B + wave * 1024);
+                // the chunk's 8 groups (16 bytes)
+                dma16(rsrc_of(upr ? bu : bg), 2u * wrow * (uint32_t)G, 16u * (uint32_t)c_pre,
+                      smem + OFF_B + wave * 1024);
             }
         }
 
@@ -523,13 +556,6 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
             for (int ni = 0; ni < 2; ++ni) {
                 // lane half 0: the biases; lane half 1: -128 x the scales of this K chunk
                 u32x4 v = fh == 0 ? (ni ? bv1 : bv0) : (ni ? sch1 : sch0);
-                if (H == 2) {  // entries 2g, 2g + 1 (two half-group sums) share group g's value
-                    const uint32_t g01 = (c_now & 1) ? v.z : v.x, g23 = (c_now & 1) ? v.w : v.y;
-                    v.x = __builtin_amdgcn_perm(g01, g01, 0x01000100u);
-                    v.y = __builtin_amdgcn_perm(g01, g01, 0x03020302u);
-                    v.z = __builtin_amdgcn_perm(g23, g23, 0x01000100u);
-                    v.w = __builtin_amdgcn_perm(g23, g23, 0x03020302u);
-                }
                 if (fh == 1) {
                     v.x = mg_neg128(v.x), v.y = mg_neg128(v.y);
                     v.z = mg_neg128(v.z), v.w = mg_neg128(v.w);
@@ -558,17 +584,15 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
         bf16_t *out = ci.sh ? j.sh.out : j.out;
         const int ldo = ci.sh ? j.sh.ldo : j.ldo;
         if (GLU) {
-            // act = R(silu(R(gate)) * R(up)), stored packed; and this wave's half-group sums of
-            // the act rows (their X split) for the down product
+            // act = R(silu(R(gate)) * R(up)), stored packed; and this wave's half of the act rows'
+            // group sums (the down product's X)
             bf16_t *OX = ci.sh ? j.sh.OX : j.OX;
-            const int oxe = 2 * (j.N / 64);
             const int col = ci.n0 + wave * 32 + fr;
             const int c64 = col & 63, kb = c64 >> 3, jj = c64 & 7;
             // lanes with jj < 4 store packed pair (jj, jj + 4) of rows i (i even); lanes jj >= 4
             // the pair of row i + 1: both at the packed position of jj & 3
             const int pcol = (col & ~63) + 8 * (2 * (kb & 3) + (kb >> 2)) + 2 * (jj & 3);
             const bool hi4 = (jj & 4) != 0;
-            const int entry = 2 * (col >> 6) + (wave & 1);
             float xsum = 0.f;  // the half-group sum of tile row `lane`
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi)
@@ -609,14 +633,13 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
                         xsum = __int_as_float(xs);
                     }
                 }
-            if (lane < ci.mrows) {
-                uint32_t hi, mid, lo;
-                split3(xsum, hi, mid, lo);
-                bf16_t *d = OX + (size_t)(ci.row0 + lane) * 3 * oxe + entry;
-                d[0] = (bf16_t)hi;
-                d[oxe] = (bf16_t)mid;
-                d[2 * oxe] = (bf16_t)lo;
-            }
+            // the group sum is this wave's half plus its partner's (waves 2h, 2h + 1 cover group
+            // n0 / 64 + h); the hand-over runs after the next barriers
+            x_pend = xsum;
+            x_dst = lane < ci.mrows
+                        ? OX + (size_t)(ci.row0 + lane) * 3 * x_oxe + (ci.n0 >> 6) + (wave >> 1)
+                        : nullptr;
+            x_state = 1;
         } else {
             // each 4 x 4 block (4 rows of a lane, 4 columns of a lane quad) is transposed within
             // the quad, so every lane stores 4 adjacent columns of one row (8 bytes)
@@ -664,6 +687,12 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
         step(gs + 3, std::integral_constant<int, 3>{});
         __builtin_amdgcn_sched_barrier(0);
     }
+    if (GLU && x_state == 1) {  // the last item's group sums
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        x_write();
+        asm volatile("s_barrier" ::: "memory");
+        x_read_store();
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the trailing copies
 }
 
@@ -678,8 +707,8 @@ bool moe_gemm_supported(const MoeGemmJob &j) {
     const int ncols = j.glu ? 128 : 256;
     if (j.N <= 0 || j.N % ncols != 0 || !ok(j.w0, j.K) || (j.glu && !ok(j.w1, j.K))) return false;
     if (j.w0.out != j.N || (j.glu && j.w1.out != j.N)) return false;
-    // X splits: one entry per group of x for gate/up, two per group of act for down
-    const int axe = (j.glu ? 1 : 2) * (j.K / 64);
+    // X splits: one entry per group of x (gate/up) or of act (down)
+    const int axe = j.K / 64;
     if (j.ax_e != axe) return false;
     if (j.has_shared) {
         if (!ok(j.sh.w0, j.K) || (j.glu && !ok(j.sh.w1, j.K))) return false;

@@ -43,10 +43,11 @@ __device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *tmp, uint32_t *to
 }
 
 // Counting blocks. Pairs are ranked inside fixed blocks of consecutive pair indices; a block's
-// per-expert bitmap (E x BP/32 words) stays within 32 KiB of LDS.
+// per-expert bitmap (E x BP/32 words) stays within 32 KiB of LDS. Blocks of at most 512 pairs
+// keep many workgroups in the scatter and a pair's rank within 16 bitmap words.
 __host__ __device__ inline int permute_block_pairs(int E) {
     int words = 8192 / (E > 0 ? E : 1);
-    if (words > 32) words = 32;
+    if (words > 16) words = 16;
     if (words < 1) words = 1;
     return 32 * words;
 }
@@ -92,30 +93,38 @@ __global__ __launch_bounds__(1024) void route_scatter_kernel(const uint32_t *__r
     __shared__ uint32_t base[1024], tbase[1024], eoff[1024], ecnt[1024], tmp[32];
     const int tid = threadIdx.x, b = blockIdx.x;
     const int W = (BP + 31) / 32;
+    // this block's ids are loaded first, then every block's counts, summed by ns threads per
+    // expert in batches of 8 loads issued before any is added, so the kernel waits for about one
+    // round trip instead of one per block
+    const int p0 = b * BP;
+    const int np = min(BP, P - p0);
+    uint32_t my_e = tid < np ? ids[p0 + tid] : 0xffffffffu;
     for (int i = tid; i < E * W; i += 1024) bm[i] = 0;
-    // the counts of every block, summed by ns threads per expert
     const int ns = E <= 1024 ? 1024 / E : 1;
     {
         const int e = tid % E, s = tid / E;
         if (s < ns) {
             uint32_t bef = 0, tot = 0;
-            for (int bb = s; bb < nb; bb += ns) {
-                const uint32_t c = counts[(size_t)bb * E + e];
-                tot += c;
-                bef += bb < b ? c : 0u;
+            for (int bb0 = s; bb0 < nb; bb0 += 8 * ns) {
+                uint32_t c[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int bb = bb0 + u * ns;
+                    c[u] = counts[(size_t)min(bb, nb - 1) * E + e];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int bb = bb0 + u * ns;
+                    tot += bb < nb ? c[u] : 0u;
+                    bef += bb < b ? c[u] : 0u;
+                }
             }
             part[0][s * E + e] = bef;
             part[1][s * E + e] = tot;
         }
     }
     __syncthreads();  // bitmaps clear, partial sums in
-    const int p0 = b * BP;
-    const int np = min(BP, P - p0);
-    uint32_t my_e = 0xffffffffu;
-    if (tid < np) {
-        my_e = ids[p0 + tid];
-        if (my_e < (uint32_t)E) atomicOr(&bm[my_e * W + (tid >> 5)], 1u << (tid & 31));
-    }
+    if (my_e < (uint32_t)E) atomicOr(&bm[my_e * W + (tid >> 5)], 1u << (tid & 31));
     uint32_t cnt = 0, bef = 0;
     if (tid < E)
         for (int s = 0; s < ns; ++s) cnt += part[1][s * E + tid], bef += part[0][s * E + tid];
