@@ -468,7 +468,10 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
             }
         }
 
-        // ---- the K step: fragments from LDS (stage ST: immediate offsets)
+        // ---- the K step: fragments from LDS (stage ST: immediate offsets). The wave raises its
+        // issue priority for the MFMA loop, so that the other workgroup's wave on this SIMD fills
+        // the matrix core's gaps with its bookkeeping rather than competing with the loop.
+        __builtin_amdgcn_s_setprio(1);
         constexpr int SA = SLOT * STAGE + (ST & 1) * A_STEP, SC = SLOT * STAGE;
         const uint32_t spar = ((gs >> 3) & 1) * S_BYTES;
         // Reads in the order they are needed; LDS reads complete in order, so a partial lgkmcnt
@@ -542,6 +545,7 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
             __builtin_amdgcn_sched_barrier(0);
         }
         sc_pend = scale_of(sch1);
+        __builtin_amdgcn_s_setprio(0);
         if (c_now >= 0) {  // bias term of chunk c_now: X splits against b (lane half 0), -128 s (1)
             const uint32_t xo = lds0 + OFF_X + 16 * fr;
             u32x4 xa00 = ds_read16<0>(xo), xa01 = ds_read16<1024>(xo), xa02 = ds_read16<2048>(xo);
