@@ -54,16 +54,26 @@ __device__ __forceinline__ void pair_x(const XRaw &r, XChunk &c) {
     c.sum = s;
 }
 
+// The code mask and the bf16 128.0 pair in VGPRs: with them as operands an and-or is one
+// v_and_or_b32 (a three-operand instruction takes no literal constant here). The asm has no side
+// effects, so the compiler computes the two values once and keeps them.
+__device__ __forceinline__ void code_consts(uint32_t &cm, uint32_t &cx) {
+    asm("v_mov_b32 %0, 0x000F000F" : "=v"(cm));
+    asm("v_mov_b32 %0, 0x43004300" : "=v"(cx));
+}
+
 // sum_k x_k (128 + q_k) over the 32 codes of one uint4.
 __device__ __forceinline__ float dot_chunk(const uint4 &q, const XChunk &x) {
     const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    uint32_t cm, cx;
+    code_consts(cm, cx);
     float acc = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        acc = dot2(x.v[4 * i + 0], (w[i] & 0x000F000Fu) | 0x43004300u, acc);
-        acc = dot2(x.v[4 * i + 1], ((w[i] >> 4) & 0x000F000Fu) | 0x43004300u, acc);
-        acc = dot2(x.v[4 * i + 2], ((w[i] >> 8) & 0x000F000Fu) | 0x43004300u, acc);
-        acc = dot2(x.v[4 * i + 3], ((w[i] >> 12) & 0x000F000Fu) | 0x43004300u, acc);
+        acc = dot2(x.v[4 * i + 0], (w[i] & cm) | cx, acc);
+        acc = dot2(x.v[4 * i + 1], ((w[i] >> 4) & cm) | cx, acc);
+        acc = dot2(x.v[4 * i + 2], ((w[i] >> 8) & cm) | cx, acc);
+        acc = dot2(x.v[4 * i + 3], ((w[i] >> 12) & cm) | cx, acc);
     }
     return acc;
 }
