@@ -72,18 +72,40 @@ __device__ __forceinline__ void gemv_wave(const QW &w0, const QW &w1, int e, int
             opaque_row(r0[g]);
             if (GLU) opaque_row(r1[g]);
         }
+        if constexpr (GLU && LPR == 64 && RG > 1) {
+            // every lane holds each row's sums; lane g finishes row g, so the wave evaluates the
+            // SwiGLU once for its RG rows
+            float s0[RG], s1[RG];
 #pragma unroll
-        for (int g = 0; g < RG; ++g) {
-            const int row = row_base + g * RPI + rsub;
-            const float a0 = group_sum<LPR>(row_part(r0[g], xc));
-            const float a1 = GLU ? group_sum<LPR>(row_part(r1[g], xc)) : 0.f;
-            if (li == 0 && row < w0.out) {
-                float v = a0;
-                if (GLU) {
-                    const float gt = rbf(a0), up = rbf(a1);
-                    v = (gt * sigmoidf_(gt)) * up;
+            for (int g = 0; g < RG; ++g) {
+                s0[g] = group_sum<64>(row_part(r0[g], xc));
+                s1[g] = group_sum<64>(row_part(r1[g], xc));
+            }
+            float a0 = s0[0], a1 = s1[0];
+#pragma unroll
+            for (int g = 1; g < RG; ++g) {
+                a0 = lane == g ? s0[g] : a0;
+                a1 = lane == g ? s1[g] : a1;
+            }
+            const int row = row_base + lane;
+            if (lane < RG && row < w0.out) {
+                const float gt = rbf(a0), up = rbf(a1);
+                out[(size_t)p * ldo + row] = (bf16_t)f2bf((gt * sigmoidf_(gt)) * up);
+            }
+        } else {
+#pragma unroll
+            for (int g = 0; g < RG; ++g) {
+                const int row = row_base + g * RPI + rsub;
+                const float a0 = group_sum<LPR>(row_part(r0[g], xc));
+                const float a1 = GLU ? group_sum<LPR>(row_part(r1[g], xc)) : 0.f;
+                if (li == 0 && row < w0.out) {
+                    float v = a0;
+                    if (GLU) {
+                        const float gt = rbf(a0), up = rbf(a1);
+                        v = (gt * sigmoidf_(gt)) * up;
+                    }
+                    out[(size_t)p * ldo + row] = (bf16_t)f2bf(v);
                 }
-                out[(size_t)p * ldo + row] = (bf16_t)f2bf(v);
             }
         }
 #pragma unroll
