@@ -8,10 +8,19 @@
 // double-buffered LDS tiles (no operand is read twice), each wave of a group owns 32 x 32 of the
 // tile, and at the end the groups' partial sums meet in LDS and are added in group order. The
 // router's products are small (T x 257 outputs: a few hundred workgroups at most, one per CU),
-// so the K steps wait on load latency: the groups put KG waves on each SIMD and shorten the chain
-// of dependent steps KG times. Each thread keeps NST K steps of loads in flight in registers (a
-// ring unrolled by NST); one barrier per K step, which waits for LDS only, so the loads stay in
-// flight across it.
+// so the K steps wait on latency: the groups put KG waves on each SIMD and shorten the chain of
+// dependent steps KG times. Each thread keeps NST K steps of loads in flight in registers (a ring
+// unrolled by NST); one barrier per K step, which waits for LDS only, so the loads stay in flight
+// across it. A step issues its MFMAs first and then stages the next step's tile, so the matrix
+// cores run while the stores and the barrier wait.
+//
+// With pack_a set, extra workgroups of the launch (column blocks past the product's, one per row
+// block and quarter of K) write A in the grouped GEMM's packed layout with launch_apack's code, bit
+// for bit. They run beside the product on the CUs it leaves idle; folded into the product's own
+// staging, their stores would share the load counter and every K step would wait for all loads.
+#include <type_traits>
+
+#include "apack.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -20,6 +29,9 @@ namespace mrun {
 namespace {
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+
+// K quarters of the packing workgroups: 4 when the quarters hold whole 64-wide groups
+__host__ __device__ inline int dense_pack_quarters(int K) { return K % 256 == 0 ? 4 : 1; }
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
 
 constexpr int DBM = 64, DBN = 64, DBK = 64, DLDK = DBK + 8;
@@ -39,8 +51,20 @@ __global__ __launch_bounds__(256 * KG) void dense_gemm_kernel(DenseJob j) {
     if (j.zero && blockIdx.x == 0 && blockIdx.y == 0)
         for (int i = threadIdx.x; i < j.n_zero; i += 256 * KG) j.zero[i] = 0;
 
-    // column block -> weight (W0's blocks first, then W1's)
+    // column block -> weight (W0's blocks first, then W1's, then the packing blocks)
     const int nb0 = (j.N0 + DBN - 1) / DBN;
+    const int nbw = nb0 + (j.W1 ? (j.N1 + DBN - 1) / DBN : 0);
+    if ((int)blockIdx.y >= nbw) {  // pack rows [64 x, +64) of K quarter y - nbw (apack's code)
+        const int nq = dense_pack_quarters(j.K), kq = (int)blockIdx.y - nbw;
+        const int bpr = j.K / nq / 8, r0 = (int)blockIdx.x * DBM;  // blocks per row and quarter
+        for (int i = threadIdx.x; i < DBM * bpr; i += 256 * KG) {
+            const int row = r0 + i / bpr, blk = kq * bpr + i % bpr;
+            // whole 64-lane waves take part in the DPP sum (bpr is a multiple of 8), rows past M
+            // are clamped for the loads and skipped for the stores
+            pack_block(j.A, j.lda, min(row, j.M - 1), row < j.M, j.K, blk, j.pack_a, j.K, j.pack_x);
+        }
+        return;
+    }
     const bool second = (int)blockIdx.y >= nb0;
     const bf16_t *W = second ? j.W1 : j.W0;
     const bf16_t *bias = second ? j.bias1 : j.bias0;
@@ -81,27 +105,34 @@ __global__ __launch_bounds__(256 * KG) void dense_gemm_kernel(DenseJob j) {
                 __builtin_bit_cast(bf16x8_t, *(const uint4 *)(a + 16 * s)),
                 __builtin_bit_cast(bf16x8_t, *(const uint4 *)(b + 16 * s)), acc, 0, 0, 0);
     };
-    // step ks: its loads (issued NST steps earlier) go to LDS buffer ks & 1, the registers are
-    // refilled with step ks + NST, then the tile is multiplied
-    auto step = [&](int ks, Stage st) __attribute__((always_inline)) -> Stage {
-        store(ks, st);
-        lds_barrier();
-        const Stage nx = load(min(ks + NST, nks - 1));  // clamped: the tail reloads a valid step
-        compute(ks);
-        return nx;
-    };
-
+    // ring slot i holds the loads of the steps = i (mod NST). Step ks (its tile in LDS buffer
+    // ks & 1) issues its MFMAs, then stores step ks + 1's loads into the other buffer and refills
+    // their slot with step ks + 1 + NST (clamped: the tail reloads a valid step), then the barrier.
     Stage ring[NST];
 #pragma unroll
     for (int i = 0; i < NST; ++i) ring[i] = load(min(i, nks - 1));
+    store(0, ring[0]);
+    ring[0] = load(min(NST, nks - 1));
+    lds_barrier();
+    auto step = [&](int ks, auto ic) __attribute__((always_inline)) {
+        constexpr int I1 = (decltype(ic)::value + 1) % NST;  // slot of step ks + 1
+        compute(ks);
+        if (ks + 1 < nks) {
+            store(ks + 1, ring[I1]);
+            ring[I1] = load(min(ks + 1 + NST, nks - 1));
+        }
+        lds_barrier();
+    };
     int ks = 0;
     for (; ks + NST <= nks; ks += NST) {
-#pragma unroll
-        for (int i = 0; i < NST; ++i) ring[i] = step(ks + i, ring[i]);
+        step(ks, std::integral_constant<int, 0>{});
+        if constexpr (NST > 1) step(ks + 1, std::integral_constant<int, 1>{});
+        if constexpr (NST > 2) step(ks + 2, std::integral_constant<int, 2>{});
+        static_assert(NST <= 3, "ring of at most 3 steps");
     }
-#pragma unroll
-    for (int i = 0; i < NST - 1; ++i)
-        if (ks + i < nks) ring[i] = step(ks + i, ring[i]);
+    if (ks < nks) step(ks, std::integral_constant<int, 0>{});
+    if constexpr (NST > 2)
+        if (ks + 1 < nks) step(ks + 1, std::integral_constant<int, 1>{});
 
     if (KG > 1) {  // group g > 0 leaves its sums in LDS; group 0 adds them in group order
         float *red = (float *)&stage_lds[0][0][0][0];
@@ -143,7 +174,8 @@ constexpr int kDenseKG = 2;
 hipError_t launch_dense_gemm(const DenseJob &j, hipStream_t stream) {
     if (!dense_gemm_supported(j.M, j.K) || j.N0 <= 0 || (j.W1 && j.N1 <= 0))
         return hipErrorInvalidValue;
-    const int nb = (j.N0 + DBN - 1) / DBN + (j.W1 ? (j.N1 + DBN - 1) / DBN : 0);
+    int nb = (j.N0 + DBN - 1) / DBN + (j.W1 ? (j.N1 + DBN - 1) / DBN : 0);
+    if (j.pack_a) nb += dense_pack_quarters(j.K);
     dim3 grid((j.M + DBM - 1) / DBM, nb);
     // a deeper ring (4, 6, 8 steps) measured no faster
     if (j.K % (DBK * kDenseKG) == 0)

@@ -241,6 +241,9 @@ struct DenseJob {
     int ldo1;
     uint32_t *zero;
     int n_zero;
+    // optional: A packed for the grouped GEMM (launch_apack's layout and bits: pack_a [M][K],
+    // pack_x [M][3][K / 64]) by extra workgroups of the same launch
+    bf16_t *pack_a, *pack_x;
 };
 bool dense_gemm_supported(int M, int K);
 hipError_t launch_dense_gemm(const DenseJob &job, hipStream_t stream);

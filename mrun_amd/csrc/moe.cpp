@@ -411,6 +411,10 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
 
     // prefill
     uint32_t *counts = (uint32_t *)at(p.counts);
+    // the grouped GEMM's packed x: written by the router launch when the router is dense, else
+    // by its own launch after the routing
+    const bool packs = mfma && T > 16 && D % 512 == 0 && I % 512 == 0;
+    bool packed = false;
     if (m.gate.weight && (!S || m.shared_expert_gate.weight) && dense_gemm_supported(T, D)) {
         // router and shared gate: one launch over x
         DenseJob dj{};
@@ -421,6 +425,7 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
             dj.N1 = 1, dj.out1 = sh_logit, dj.ldo1 = 1;
         }
         dj.zero = counts, dj.n_zero = p.n_counts;
+        if (packs) dj.pack_a = (bf16_t *)at(p.xp), dj.pack_x = (bf16_t *)at(p.xs), packed = true;
         TRY_HIP(launch_dense_gemm(dj, s), "router (mfma)");
         st.mark(s);  // (the shared gate's stage below stays empty: it ran in this launch)
     } else {
@@ -435,10 +440,9 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
     PermuteOut pt = po;
     pt.tiles = (uint32_t *)at(p.tiles);
     pt.n_tiles = (uint32_t *)at(p.n_tiles);
-    const bool packs = mfma && T > 16 && D % 512 == 0 && I % 512 == 0;
     if (packs) pt.tile_rows = (uint32_t *)at(p.tile_rows);
     TRY_HIP(launch_route_scatter(ids, counts, T, k, E, pt, s), "scatter");
-    if (packs)
+    if (packs && !packed)
         TRY_HIP(launch_apack(x, D, T, D, (bf16_t *)at(p.xp), D, (bf16_t *)at(p.xs), s), "pack x");
     st.mark(s);
     // the grouped GEMM of moe_gemm.hip: 4-bit group-64 experts, K a multiple of 512, the shared

@@ -30,6 +30,7 @@
 // vmcnt counts, so the compiler inserts no wait of its own on the LDS that the DMA fills.
 #include <type_traits>
 
+#include "apack.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -116,16 +117,6 @@ __device__ __forceinline__ uint32_t mg_neg128(uint32_t w) {
     return lo | hi;
 }
 
-// X split exactly into three bf16: hi + mid + lo == x (truncations of f32)
-__device__ __forceinline__ void split3(float x, uint32_t &hi, uint32_t &mid, uint32_t &lo) {
-    const float h = __uint_as_float(__float_as_uint(x) & 0xFFFF0000u);
-    const float r1 = x - h;
-    const float m = __uint_as_float(__float_as_uint(r1) & 0xFFFF0000u);
-    hi = __float_as_uint(h) >> 16;
-    mid = __float_as_uint(m) >> 16;
-    lo = __float_as_uint(r1 - m) >> 16;
-}
-
 // ---------------------------------------------------------------------------------------------
 // A packing: x [rows][K] (row stride lda) -> packed rows [rows][K] (stride ldp) and the X splits
 // [rows][3][K / 64]. One thread per 8-element block; the 8 threads of a group are adjacent lanes.
@@ -136,28 +127,7 @@ __global__ __launch_bounds__(256) void apack_kernel(const bf16_t *__restrict__ x
     const int nb = K / 8;
     const long long b = (long long)blockIdx.x * 256 + threadIdx.x;
     if (b >= (long long)rows * nb) return;  // whole groups only: rows * nb is a multiple of 8
-    const int row = (int)(b / nb), blk = (int)(b % nb), g = blk >> 3, w = blk & 7;
-    const uint4 v = *(const uint4 *)(x + (size_t)row * lda + (size_t)blk * 8);
-    const uint4 p = make_uint4(__builtin_amdgcn_perm(v.z, v.x, 0x05040100u),
-                               __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
-                               __builtin_amdgcn_perm(v.w, v.y, 0x05040100u),
-                               __builtin_amdgcn_perm(v.w, v.y, 0x07060302u));
-    const int pos = 2 * (w & 3) + (w >> 2);
-    *(uint4 *)(xp + (size_t)row * ldp + g * 64 + pos * 8) = p;
-    float s = bf_lo(v.x) + bf_hi(v.x);
-    s += bf_lo(v.y) + bf_hi(v.y);
-    s += bf_lo(v.z) + bf_hi(v.z);
-    s += bf_lo(v.w) + bf_hi(v.w);
-    s = group_sum<8>(s);
-    if (w == 0) {
-        uint32_t hi, mid, lo;
-        split3(s, hi, mid, lo);
-        const int G = K / 64;
-        bf16_t *d = xs + (size_t)row * 3 * G + g;
-        d[0] = (bf16_t)hi;
-        d[G] = (bf16_t)mid;
-        d[2 * G] = (bf16_t)lo;
-    }
+    pack_block(x, lda, (int)(b / nb), true, K, (int)(b % nb), xp, ldp, xs);
 }
 
 hipError_t launch_apack(const bf16_t *x, int lda, int rows, int K, bf16_t *xp, int ldp,
