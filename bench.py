@@ -645,6 +645,22 @@ def main(argv=None) -> int:
             p, _ = decode_point(T, max(args.steps // 2, 20), args.warmup)
             sweep.append(p)
 
+    # mlx-community conversions store the router and the shared-expert gate in 8 bits (group 64):
+    # the same block with those two quantized, decode T = 1 and 16
+    gates8 = None
+    if not args.no_sweep:
+        print("[bench] decode with an 8-bit router and shared gate", file=sys.stderr, flush=True)
+        h8 = synth.make_block(Q, config=synth.CFG_DECODE, gate_bits=8)
+        d8 = M.SparseMoe(h8)
+        gates8 = {"weights": "router and shared-expert gate 8-bit affine, group 64; experts as "
+                             "configs[1]"}
+        for T in (1, 16):
+            x8 = M.bf16_tensor(synth.make_x(Q, T, config=synth.CFG_DECODE, layer=T))
+            wall, dev_ms, _ = time_forward(d8, x8, max(args.steps // 2, 20), args.warmup, torch)
+            gates8[f"T{T}"] = {"tokens": T, "device_ms": dev_ms, "ms_per_step": wall,
+                               "tokens_per_s": T / (wall * 1e-3)}
+        del d8, h8
+
     prefill = None if args.no_prefill else prefill_point(args, Q, M, synth, torch)
     stack = None if args.no_stack else stack_point(args, Q, M, synth, torch)
     coder = None if args.no_coder else coder_point(args, M, synth, torch, cold)
@@ -689,6 +705,7 @@ def main(argv=None) -> int:
         "cpu_baseline": cpu,
         "machine": machine,
         "sweep": sweep,
+        "gates8": gates8,
         "prefill": prefill,
         "stack": stack,
         "coder": coder,

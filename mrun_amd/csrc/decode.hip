@@ -255,22 +255,101 @@ hipError_t launch_rows(const bf16_t *x, int T, int D, const bf16_t *W, const bf1
     return hipGetLastError();
 }
 
+// One quantized Linear row (4 or 8 bits, expert 0 of w; groups of 32 to 128) for T <= 16 tokens:
+// R(x[t] . w) then R(. + bias), the weight dequantized as q s + b in f32 (Quantized::dequantize,
+// nuvec.rs:1173-1204) and dotted in f32. Lane l owns the 8-element chunks [8l + 512i, +8) of each
+// 2048-wide pass (a chunk lies in one group); all of a pass's loads are issued before any is used.
+template <int MAXT>
+__device__ __forceinline__ void qrouter_row(const bf16_t *x, int T, int D, const QW &w, int row,
+                                            const bf16_t *bias, bf16_t *out, int ldo, int lane) {
+    float acc[MAXT];
+#pragma unroll
+    for (int t = 0; t < MAXT; ++t) acc[t] = 0.f;
+    const int groups = D / w.group, wpr = D * w.bits / 32;  // code words per row
+    const uint32_t *codes = w.codes + (size_t)row * wpr;
+    const bf16_t *sc = w.scales + (size_t)row * groups;
+    const bf16_t *bi = w.biases ? w.biases + (size_t)row * groups : nullptr;
+    for (int d0 = lane * 8; d0 < D; d0 += 2048) {
+        uint2 cw[4];
+        uint32_t sraw[4], braw[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int d = min(d0 + 512 * i, D - 8);  // clamped; chunks past D are not used
+            if (w.bits == 8) cw[i] = *(const uint2 *)(codes + d / 4);
+            else cw[i] = make_uint2(codes[d / 8], 0u);
+            sraw[i] = sc[d / w.group];
+            braw[i] = bi ? bi[d / w.group] : 0u;
+        }
+        float wv[4][8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float s = bf2f(sraw[i]), b = bf2f(braw[i]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t q = w.bits == 8 ? ((e < 4 ? cw[i].x : cw[i].y) >> (8 * (e & 3))) & 0xFFu
+                                               : (cw[i].x >> (4 * e)) & 0xFu;
+                wv[i][e] = __builtin_fmaf((float)q, s, b);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < MAXT; ++t) {
+            if (t < T) {
+                uint4 xv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    xv[i] = *(const uint4 *)(x + (size_t)t * D + min(d0 + 512 * i, D - 8));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (d0 + 512 * i < D) {
+                        float xf[8];
+                        unpack8(xv[i], xf);
+                        float a = acc[t];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) a = __builtin_fmaf(xf[e], wv[i][e], a);
+                        acc[t] = a;
+                    }
+                }
+            }
+        }
+    }
+    const uint32_t braw = bias ? (uint32_t)*bias : 0u;
+#pragma unroll
+    for (int t = 0; t < MAXT; ++t) {
+        if (t < T) {
+            const float v = group_sum<64>(acc[t]);
+            if (lane == 0) {
+                float l = rbf(v);
+                if (bias) l = rbf(l + bf2f(braw));
+                out[(size_t)t * ldo] = (bf16_t)f2bf(l);
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------------------------
 // K1: router logits + the shared expert's gate logit
 
-template <int MAXT, bool NORM>
+// QUANT: some rows are quantized (a separate instantiation, so the dense-router kernel keeps its
+// registers and schedule)
+template <int MAXT, bool NORM, bool QUANT>
 __global__ __launch_bounds__(256) void decode_router_kernel(DecodeJob j) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = blockIdx.x * 4 + wave;
     const int D = j.D;
     const bf16_t *w = nullptr, *bias = nullptr;
+    const QW *qw = nullptr;  // a quantized row instead (row qr of it)
+    int qr = 0;
     bf16_t *out = nullptr;
     int ldo = 1;
     if (r < j.E) {
-        w = j.router + (size_t)r * D, out = j.logits + r, ldo = j.E;
+        if (!QUANT || j.router) w = j.router + (size_t)r * D;
+        else qw = &j.router_q, qr = r;
+        out = j.logits + r, ldo = j.E;
         bias = j.router_bias ? j.router_bias + r : nullptr;
     } else if (r == j.E && j.S) {
-        w = j.sh_gate_w, bias = j.sh_gate_b, out = j.sh_logit;
+        if (!QUANT || j.sh_gate_w) w = j.sh_gate_w;
+        else qw = &j.sh_gate_q;
+        bias = j.sh_gate_b, out = j.sh_logit;
     }
     // the weight row's first pass is loaded before anything waits (the norm below, in particular)
     Row4 first{};
@@ -320,6 +399,7 @@ __global__ __launch_bounds__(256) void decode_router_kernel(DecodeJob j) {
         x = hs;
     }
     if (w) router_row<MAXT>(x, j.T, D, w, first, bias, out, ldo, lane);
+    else if (QUANT && qw) qrouter_row<MAXT>(x, j.T, D, *qw, qr, bias, out, ldo, lane);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -674,9 +754,15 @@ static int stream_k3_rows(const DecodeJob &j) {
 template <int MAXT>
 static void launch_k1(const DecodeJob &j, hipStream_t s) {
     dim3 grid((j.E + (j.S ? 1 : 0) + 3) / 4);
-    if (j.norm_src)
-        decode_router_kernel<MAXT, true><<<grid, 256, 2 * (size_t)j.T * j.D, s>>>(j);
-    else decode_router_kernel<MAXT, false><<<grid, 256, 0, s>>>(j);
+    const size_t lds = j.norm_src ? 2 * (size_t)j.T * j.D : 0;
+    if (!j.router || (j.S && !j.sh_gate_w)) {  // a quantized router or shared gate
+        if (j.norm_src) decode_router_kernel<MAXT, true, true><<<grid, 256, lds, s>>>(j);
+        else decode_router_kernel<MAXT, false, true><<<grid, 256, 0, s>>>(j);
+    } else if (j.norm_src) {
+        decode_router_kernel<MAXT, true, false><<<grid, 256, lds, s>>>(j);
+    } else {
+        decode_router_kernel<MAXT, false, false><<<grid, 256, 0, s>>>(j);
+    }
 }
 
 template <int LPR, int CPL, int PB, int DR>

@@ -123,6 +123,9 @@ struct DecodeJob {
     const bf16_t *x;
     int T, D, E, k, I, S, norm, max_slots;
     const bf16_t *router, *router_bias, *sh_gate_w, *sh_gate_b;
+    // a quantized router or shared gate (4 or 8 bits; router null / sh_gate_w null): K1 dequantizes
+    // its rows itself (mlx-community conversions store both in 8 bits)
+    QW router_q, sh_gate_q;
     QW wg, wu, wd, sg, su, sd;
     bf16_t *logits;   // [T, E]
     uint32_t *ids;    // [T, k] and

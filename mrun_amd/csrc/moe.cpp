@@ -312,6 +312,11 @@ static const char *kDecodeStages = "router,gate_up,down_combine";
 static const char *kPrefillStages =
     "router,shared_gate,topk,permute,gate_up,down,shared_gate_up,shared_down,combine";
 
+// whether the decode router launch takes this Linear: dense bf16, or 4/8-bit quantized
+static bool k1_router_ok(const mrun_linear &l) {
+    return l.weight || l.q.bits == 4 || l.q.bits == 8;
+}
+
 static bool is_decode(const mrun_moe_config &c, int T) {
     return decode_supported(c.hidden, c.intermediate, c.shared_intermediate, T, c.top_k,
                             c.experts);
@@ -393,14 +398,20 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
         }
         j.logits = logits, j.sh_logit = sh_logit, j.sh_act = sh_act, j.act = act, j.out = out;
         j.ids = ids, j.scores = scores, j.topk_in_kernel = T <= 4;
+        // a quantized router or shared gate (8-bit in mlx-community conversions): K1 dequantizes
+        // its rows (4 or 8 bits; the checked group sizes keep a lane's 8-element chunks in one
+        // group)
+        const bool r_ok = k1_router_ok(m.gate);
+        const bool g_ok = !S || k1_router_ok(m.shared_expert_gate);
+        if (!m.gate.weight && r_ok) j.router_q = qw_of(m.gate.q);
+        if (S && !m.shared_expert_gate.weight && g_ok) j.sh_gate_q = qw_of(m.shared_expert_gate.q);
         if (fn) {  // K1 normalises fn->src into x; K3 adds the residual
-            if (!m.gate.weight || (S && !m.shared_expert_gate.weight))
-                return Err(MRUN_ERR_UNSUPPORTED, "fused norm needs a dense router and shared gate");
+            if (!r_ok || !g_ok)
+                return Err(MRUN_ERR_UNSUPPORTED,
+                           "fused norm needs a dense or 4/8-bit router and shared gate");
             j.norm_src = fn->src, j.norm_w = fn->w, j.eps = fn->eps, j.residual = fn->src;
         }
-        // quantized router or shared gate (8-bit in mlx-community conversions): their logits come
-        // from the generic products, and the decode launches start at the routed experts
-        if (!fn && (!m.gate.weight || (S && !m.shared_expert_gate.weight))) {
+        if (!r_ok || !g_ok) {
             TRY(tensor::linear(x, T, m.gate, logits, s));
             if (S) TRY(tensor::linear(x, T, m.shared_expert_gate, sh_logit, s));
             j.router_done = 1;
@@ -930,13 +941,14 @@ int mrun_moe_stack_forward(const mrun_sparse_moe *layers, int32_t n_layers,
         bf16_t *o = (bf16_t *)(ws + blk + a256(2 * (size_t)tokens * D));
         hipStream_t s = (hipStream_t)stream;
         auto wl = [&](int l) { return norm_w ? norm_w[l] : nullptr; };
-        // decode-sized chunks with dense routers: the norm runs inside each block's router launch
-        // and the residual add inside its last launch (three launches per layer, no norm kernel)
+        // decode-sized chunks with dense or 4/8-bit routers: the norm runs inside each block's
+        // router launch and the residual add inside its last launch (three launches per layer,
+        // no norm kernel)
         bool fused = models::is_decode(layers[0], tokens) &&
                      2 * (size_t)tokens * D <= 65536;  // the normalised rows fit the router's LDS
         for (int32_t l = 0; fused && l < n_layers; ++l)
-            fused = layers[l].gate.weight && (c.shared_intermediate == 0 ||
-                                              layers[l].shared_expert_gate.weight);
+            fused = models::k1_router_ok(layers[l].gate) &&
+                    (c.shared_intermediate == 0 || models::k1_router_ok(layers[l].shared_expert_gate));
         for (int32_t l = 0; fused && st.ok() && l < n_layers; ++l) {
             const models::FusedNorm fn{x, wl(l), eps};
             st = models::sparse_moe_forward(layers[l], h, tokens, x, ws, blk, s, nullptr, &fn);

@@ -413,6 +413,13 @@ def stack3():
     return hosts, M.MoeStack([M.SparseMoe(h) for h in hosts])
 
 
+@pytest.fixture(scope="module")
+def stack3_gates8():
+    hosts = [synth.make_block(STACK, config=synth.CFG_STACK, layer=10 + l, gate_bits=8)
+             for l in range(3)]
+    return hosts, M.MoeStack([M.SparseMoe(h) for h in hosts])
+
+
 @pytest.mark.parametrize("T", [4, 40])
 def test_stack_matches_layer_loop_and_oracle(stack3, T):
     """configs[3]'s decoder-layer loop, x = R(x + MoE_l(rms_norm(x))) per layer, with layer l's
@@ -421,7 +428,18 @@ def test_stack_matches_layer_loop_and_oracle(stack3, T):
     layer by layer on the GPU's expert choices (each validated as a top-k within ties): within the
     block bar plus one bf16 ulp of the residual stream (a rounding of x + MoE(h) that lands on the
     neighbouring value moves x by one ulp of |x|, which exceeds 2e-2 where |x| >= 4)."""
-    hosts, st = stack3
+    _check_stack(stack3, T, "stack")
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_stack_8bit_gates(stack3_gates8, T):
+    """The same loop with 8-bit group-64 routers and shared gates (mlx-community conversions):
+    at decode sizes the router launch dequantizes their rows itself, with the norm fused."""
+    _check_stack(stack3_gates8, T, "stack, 8-bit gates")
+
+
+def _check_stack(stack, T, label):
+    hosts, st = stack
     x_np = synth.make_x(STACK, T, config=synth.CFG_STACK, layer=T)
     got = M.bf16_bits(st.forward_(M.bf16_tensor(x_np)))
     x = M.bf16_tensor(x_np)
@@ -440,13 +458,13 @@ def test_stack_matches_layer_loop_and_oracle(stack3, T):
     g, r = synth.bf16_to_f32(got).astype(np.float64), synth.bf16_to_f32(ref).astype(np.float64)
     bound = 2e-2 + bf16_ulp(np.maximum(np.abs(g), np.abs(r)))
     s = stats(got, ref)
-    assert np.all(np.abs(g - r) <= bound), f"stack T={T}: {s}"
-    assert s["l1_rel"] <= 1e-3, f"stack T={T}: {s}"
+    assert np.all(np.abs(g - r) <= bound), f"{label} T={T}: {s}"
+    assert s["l1_rel"] <= 1e-3, f"{label} T={T}: {s}"
     # the oracle's own stack entry agrees with its layer loop
     if T == 4:
         own = O.moe_stack(hosts, x_np, None, 1e-6)
         _log(f"oracle stack vs GPU: {stats(got, own)}")
-    _log(f"stack of 3, T={T}: {s}")
+    _log(f"{label} of 3, T={T}: {s}")
 
 
 # ---------------------------------------------------------------------------------------------
