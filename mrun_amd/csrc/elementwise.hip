@@ -139,9 +139,63 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const bf16_t *x,
     }
 }
 
+// Rows of at most 2048: one wave per row (four rows per workgroup). The wave reads its row once
+// into registers (lane l: elements [8l + 512i, +8)), forms 1/rms with row_rms_inv's order and
+// rounding (the same bits as the kernel above and the fused decode router) and writes the elements
+// it read, so h may alias x or res.
+__global__ __launch_bounds__(256) void rms_norm_row_kernel(const bf16_t *x, const bf16_t *res,
+                                                           const bf16_t *__restrict__ w, int rows,
+                                                           int D, float eps, bf16_t *h,
+                                                           bf16_t *__restrict__ y) {
+    const int lane = threadIdx.x & 63, r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const bf16_t *xr = x + (size_t)r * D;
+    const bf16_t *rr = res ? res + (size_t)r * D : nullptr;
+    uint4 xv[4], rv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int d = min(lane * 8 + 512 * i, D - 8);  // clamped; chunks past D are not used
+        xv[i] = *(const uint4 *)(xr + d);
+        rv[i] = rr ? *(const uint4 *)(rr + d) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    float f[4][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        unpack8(xv[i], f[i]);
+        if (rr) {
+            float rf[8];
+            unpack8(rv[i], rf);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) f[i][k] = rbf(f[i][k] + rf[k]);
+        }
+        if (lane * 8 + 512 * i < D) ss = sumsq8(f[i], ss);
+    }
+    const float inv = rms_inv_of(group_sum<64>(ss), D, eps);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int d = lane * 8 + 512 * i;
+        if (d >= D) continue;
+        uint32_t o[8], hv[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float wv = w ? bf2f(w[d + k]) : 1.0f;
+            o[k] = f2bf(rbf(f[i][k] * inv) * wv);
+            hv[k] = f2bf(f[i][k]);
+        }
+        if (rr && h)
+            *(uint4 *)(h + (size_t)r * D + d) =
+                make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16),
+                           hv[6] | (hv[7] << 16));
+        *(uint4 *)(y + (size_t)r * D + d) = make_uint4(
+            o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16));
+    }
+}
+
 hipError_t launch_rms_norm(const bf16_t *x, const bf16_t *res, const bf16_t *w, int rows, int D,
                            float eps, bf16_t *h, bf16_t *y, hipStream_t stream) {
-    rms_norm_kernel<<<rows, 256, 0, stream>>>(x, res, w, D, eps, h, y);
+    if (D <= 2048) rms_norm_row_kernel<<<(rows + 3) / 4, 256, 0, stream>>>(x, res, w, rows, D, eps, h, y);
+    else rms_norm_kernel<<<rows, 256, 0, stream>>>(x, res, w, D, eps, h, y);
     return hipGetLastError();
 }
 
