@@ -64,21 +64,23 @@ static_assert(LDS_BYTES <= 81920, "two workgroups per CU");
 __device__ __forceinline__ uint32_t lds_offset(const void *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
 }
+// An LDS read whose wait comes later (an lgkmcnt asm taking the destination as "+v"). The compiler
+// takes the destination as written at issue, so any copy or spill of it before the wait would read
+// a register the load has not yet filled: the kernels that use it must build without VGPR spills
+// (tests/test_isa.py checks the built code for both).
 template <int OFF>
 __device__ __forceinline__ u32x4 ds_read16(uint32_t a) {
     u32x4 v;
     asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
     return v;
 }
-__device__ __forceinline__ uint32_t ds_read4(uint32_t a) {
-    uint32_t v;
-    asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(a));
-    return v;
-}
-__device__ __forceinline__ uint32_t ds_read2(uint32_t a) {
-    uint32_t v;
-    asm volatile("ds_read_u16 %0, %1" : "=v"(v) : "v"(a));
-    return v;
+// Reads whose results become addresses or counts: the reads and their wait are one statement, so
+// that no copy or spill of a destination register can come between a read and its arrival.
+__device__ __forceinline__ void ds_read3_now(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t &v0,
+                                             uint32_t &v1, uint32_t &v2) {
+    asm volatile("ds_read_b32 %0, %3\n\tds_read_b32 %1, %4\n\tds_read_b32 %2, %5\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(v0), "=&v"(v1), "=&v"(v2)
+                 : "v"(a0), "v"(a1), "v"(a2));
 }
 // Global memory goes to LDS through buffer loads (buffer_load ... lds): a raw resource per
 // tensor (base address in scalar registers), a per-lane 32-bit byte offset and a scalar one, so
@@ -212,8 +214,8 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
             const int r = rt - s_tiles;
             if (j.has_routing) {
                 const uint32_t rec = lds0 + OFF_T + (uint32_t)(n & 1) * T_BYTES;
-                uint32_t e = ds_read4(rec), row0 = ds_read4(rec + 4), mrows = ds_read4(rec + 8);
-                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(e), "+v"(row0), "+v"(mrows));
+                uint32_t e, row0, mrows;
+                ds_read3_now(rec, rec + 4, rec + 8, e, row0, mrows);
                 it.e = uni((int)e), it.row0 = uni((int)row0), it.mrows = uni((int)mrows);
                 it.tile = j.tile_rows ? r : -1;
             } else {
@@ -239,11 +241,18 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
     Item li{};     // the load cursor's item, taken over by the compute cursor at its switch
     int lx = 0;    // the load cursor's A row of tile row `lane` (the bias term's X splits)
 
-    // the A row (token) of tile row r of item n
-    auto a_row = [&](const Item &it, int n, int r) __attribute__((always_inline)) -> int {
-        const int rr = min(r, it.mrows - 1);
-        if (it.tile >= 0) return (int)ds_read4(lds0 + OFF_R + (n & 1) * R_BYTES + 4 * rr);
-        return it.row0 + rr;
+    // the A rows (tokens) of tile rows r0, r1, r2 of item n
+    auto a_rows = [&](const Item &it, int n, int r0, int r1, int r2, int &v0, int &v1, int &v2)
+                      __attribute__((always_inline)) {
+        r0 = min(r0, it.mrows - 1), r1 = min(r1, it.mrows - 1), r2 = min(r2, it.mrows - 1);
+        if (it.tile >= 0) {
+            const uint32_t rb = lds0 + OFF_R + (uint32_t)(n & 1) * R_BYTES;
+            uint32_t u0, u1, u2;
+            ds_read3_now(rb + 4 * r0, rb + 4 * r1, rb + 4 * r2, u0, u1, u2);
+            v0 = (int)u0, v1 = (int)u1, v2 = (int)u2;
+        } else {
+            v0 = it.row0 + r0, v1 = it.row0 + r1, v2 = it.row0 + r2;
+        }
     };
     // copy item n's tile record and token rows into LDS slot n % 2 (wave 0; routed tiles)
     auto fetch_rows = [&](int n) __attribute__((always_inline)) {
@@ -260,8 +269,8 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
     };
     auto setup_load = [&](int n) __attribute__((always_inline)) {
         const Item it = item_of(n);
-        int r0 = a_row(it, n, ra), r1 = a_row(it, n, ra + 32), x0 = a_row(it, n, lane);
-        if (it.tile >= 0) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r0), "+v"(r1), "+v"(x0));
+        int r0, r1, x0;
+        a_rows(it, n, ra, ra + 32, lane, r0, r1, x0);
         li = it, lx = x0;
         const int lda = it.sh ? j.sh.lda : j.lda;
         r_a = rsrc_of(it.sh ? j.sh.A : j.A);
@@ -375,8 +384,8 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
     };
     auto x_read_store = [&]() __attribute__((always_inline)) {
         if (!(wave & 1)) {
-            uint32_t o = ds_read4(x_slot);
-            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(o));
+            uint32_t o;
+            asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(o) : "v"(x_slot));
             if (x_dst) {
                 uint32_t hi, mid, lo;
                 split3(x_pend + __uint_as_float(o), hi, mid, lo);
