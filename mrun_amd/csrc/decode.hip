@@ -405,7 +405,7 @@ __global__ __launch_bounds__(256) void decode_router_kernel(DecodeJob j) {
 // ---------------------------------------------------------------------------------------------
 // shared by K2 and K3: the top-k of every token into LDS, and the active-expert mask
 
-template <int NW>
+template <int NW, bool MASK = true>
 __device__ __forceinline__ void all_topk(const DecodeJob &j, bool compute, uint32_t *sid,
                                          bf16_t *ssc, uint32_t *mask) {
     // token t goes to wave (t + blockIdx.x) % NW: the workgroups sharing a CU spread their top-k
@@ -424,6 +424,7 @@ __device__ __forceinline__ void all_topk(const DecodeJob &j, bool compute, uint3
         }
     }
     __syncthreads();
+    if (!MASK) return;
     for (int p = threadIdx.x; p < j.T * j.k; p += 64 * NW) atomicOr(&mask[sid[p] >> 5], 1u << (sid[p] & 31));
     __syncthreads();
 }
@@ -517,7 +518,11 @@ __attribute__((amdgpu_waves_per_eu(LOOP && CPL == 3 ? 3 : 1))) void decode_gateu
         const int r = blockIdx.x - n_sh, row_blocks = j.I / (NW * RG * RPI * L);
         const int slot = r / row_blocks;
         rb = r % row_blocks;
-        all_topk<NW>(j, j.topk_in_kernel != 0, sid, ssc, mask);
+        // one token (the T = 1 decode): its k experts are distinct, so slot s takes the s-th ranked
+        // one, pair s; no expert mask and no search of it on the way to the expert rows
+        const bool one = j.T == 1 && j.topk_in_kernel;
+        if (one) all_topk<NW, false>(j, true, sid, ssc, mask);
+        else all_topk<NW>(j, j.topk_in_kernel != 0, sid, ssc, mask);
         if (r == 0 && j.topk_in_kernel) {  // publish the routing for K3
             const int P = j.T * j.k;
             if ((int)threadIdx.x < P) {
@@ -525,9 +530,15 @@ __attribute__((amdgpu_waves_per_eu(LOOP && CPL == 3 ? 3 : 1))) void decode_gateu
                 j.scores[threadIdx.x] = ssc[threadIdx.x];
             }
         }
-        e = slot_expert(mask, (j.E + 31) / 32, slot, lane);
-        if (e < 0) return;
-        pairs_of(sid, j.T * j.k, e, lane, pm0, pm1);
+        if (one) {
+            if (slot >= j.k) return;
+            e = __builtin_amdgcn_readfirstlane((int)sid[slot]);
+            pm0 = 1ull << slot, pm1 = 0;
+        } else {
+            e = slot_expert(mask, (j.E + 31) / 32, slot, lane);
+            if (e < 0) return;
+            pairs_of(sid, j.T * j.k, e, lane, pm0, pm1);
+        }
         a_div = j.k, ldo = j.I, out = j.act;
     }
     if (LOOP) {  // RG = 1, LPR = 64: rows rb * L * NW + wave + NW * l, pair by pair
