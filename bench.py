@@ -94,18 +94,29 @@ def prefill_flops(shape, T: int) -> dict:
 
 
 def time_forward(dev, x, steps: int, warmup: int, torch):
-    """Wall clock and HIP-event time of `steps` forwards (after `warmup`)."""
+    """Wall clock and HIP-event time of `steps` forwards (after `warmup`). Each forward is one call
+    of the C ABI's mrun_moe_forward with its arguments converted once, as a native host calls it:
+    the Python wrapper's per-call work (about 1.5 us) would otherwise set the pace of the T = 1
+    forward, whose three launches take the host about 13 us against 14 us on the device."""
+    from mrun_amd import _lib
     stream = torch.cuda.current_stream()
     out = torch.empty_like(x)
     ws = dev.workspace(x.shape[0])
     for _ in range(warmup):
         dev.forward(x, out=out, workspace=ws)
+    fwd = _lib.load().mrun_moe_forward
+    args = (ctypes.byref(dev.c), ctypes.c_void_p(x.data_ptr()), x.shape[0],
+            ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+            ctypes.c_void_p(stream.cuda_stream))
+    _lib.check(fwd(*args))
     ev = Events(2)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev.record(0, stream)
+    rc = 0
     for _ in range(steps):
-        dev.forward(x, out=out, workspace=ws)
+        rc |= fwd(*args)
+    _lib.check(rc)
     ev.record(1, stream)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps

@@ -479,7 +479,7 @@ __host__ __device__ inline int shared_gateup_blocks(const DecodeJob &j, int rows
 
 // (the streaming kernel with 3 chunks per lane is held to 168 registers, 3 waves per SIMD: at 171
 // it ran 2, and T = 1 took 4 us longer on the Coder shape)
-template <int LPR, int CPL, int RG, int NW, bool LOOP>
+template <int LPR, int CPL, int RG, int NW, bool LOOP, bool SH_LAST>
 __global__ __launch_bounds__(64 * NW)
 __attribute__((amdgpu_waves_per_eu(LOOP && CPL == 3 ? 3 : 1))) void decode_gateup_kernel(
     DecodeJob j) {
@@ -490,7 +490,13 @@ __attribute__((amdgpu_waves_per_eu(LOOP && CPL == 3 ? 3 : 1))) void decode_gateu
     const int L = LOOP ? j.gu_loop : 1;
     const int n_sh = shared_gateup_blocks(j, NW * RG * RPI * L);
     // one gemv_wave call for both kinds of workgroup (its code is large): pick its operands
-    const bool sh = (int)blockIdx.x < n_sh;
+    // Workgroup order. A CU hosts two or three K2 workgroups (i, i + #CUs, ...), and its later ones
+    // run slower. SH_LAST (T <= 2) puts the routed workgroups first, so that the shared ones (no
+    // routing to wait for, done early) take the CUs' third places; above, where the shared
+    // expert's share is larger, they go first.
+    const int n_ro = (int)gridDim.x - n_sh;
+    const bool sh = SH_LAST ? (int)blockIdx.x >= n_ro : (int)blockIdx.x < n_sh;
+    const int bid = !SH_LAST ? (int)blockIdx.x : sh ? (int)blockIdx.x - n_ro : (int)blockIdx.x + n_sh;
     auto pick = [&](const QW &a, const QW &b) {  // field by field: no copy of the arguments
         QW q;
         q.codes = sh ? a.codes : b.codes;
@@ -509,13 +515,13 @@ __attribute__((amdgpu_waves_per_eu(LOOP && CPL == 3 ? 3 : 1))) void decode_gateu
     bf16_t *out;
     if (sh) {  // shared expert gate/up: 4 * RG * RPI rows x up to 4 tokens
         const int n_row_blocks = j.S / (NW * RG * RPI * L);
-        rb = blockIdx.x % n_row_blocks;
-        const int t0 = (blockIdx.x / n_row_blocks) * 4;
+        rb = bid % n_row_blocks;
+        const int t0 = (bid / n_row_blocks) * 4;
         const int tn = min(4, j.T - t0);
         a_div = 1, ldo = j.S, out = j.sh_act;
         pm0 = ((1ull << tn) - 1) << t0, pm1 = 0;
     } else {
-        const int r = blockIdx.x - n_sh, row_blocks = j.I / (NW * RG * RPI * L);
+        const int r = bid - n_sh, row_blocks = j.I / (NW * RG * RPI * L);
         const int slot = r / row_blocks;
         rb = r % row_blocks;
         // one token (the T = 1 decode): its k experts are distinct, so slot s takes the s-th ranked
@@ -789,16 +795,22 @@ static void launch_k3_pb(const DecodeJob &j, hipStream_t s);
 template <int RG, int NW, bool LOOP>
 static void launch_k2_l(const DecodeJob &j, int n_ch, dim3 g2, hipStream_t s,
                         const StageMarks *marks) {
-    auto go = [&](auto kernel) {
+    auto go1 = [&](auto kernel) {
         if (marks && marks->k2_start)  // timed by the launch itself (benchmark instrumentation)
             hipExtLaunchKernelGGL(kernel, g2, dim3(64 * NW), 0, s, marks->k2_start, marks->k2_stop,
                                   0, j);
         else kernel<<<g2, 64 * NW, 0, s>>>(j);
     };
-    if (n_ch <= 64) go(decode_gateup_kernel<64, 1, RG, NW, LOOP>);
-    else if (n_ch <= 128) go(decode_gateup_kernel<64, 2, RG, NW, LOOP>);
-    else if (n_ch <= 192) go(decode_gateup_kernel<64, 3, RG, NW, LOOP>);
-    else go(decode_gateup_kernel<64, 4, RG, NW, LOOP>);
+    // the shared expert's workgroups last at T <= 2 (T = 1: 14.9 -> 14.2 us per block, T = 2:
+    // 20.8 -> 19.3), first above (last measured 4 and 7 us slower at T = 4 and 16)
+    auto go = [&](auto first, auto last) {
+        if (j.T <= 2) go1(last);
+        else go1(first);
+    };
+    if (n_ch <= 64) go(decode_gateup_kernel<64, 1, RG, NW, LOOP, false>, decode_gateup_kernel<64, 1, RG, NW, LOOP, true>);
+    else if (n_ch <= 128) go(decode_gateup_kernel<64, 2, RG, NW, LOOP, false>, decode_gateup_kernel<64, 2, RG, NW, LOOP, true>);
+    else if (n_ch <= 192) go(decode_gateup_kernel<64, 3, RG, NW, LOOP, false>, decode_gateup_kernel<64, 3, RG, NW, LOOP, true>);
+    else go(decode_gateup_kernel<64, 4, RG, NW, LOOP, false>, decode_gateup_kernel<64, 4, RG, NW, LOOP, true>);
 }
 
 template <int RG, int NW>
