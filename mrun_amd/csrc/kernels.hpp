@@ -62,8 +62,8 @@ struct PermuteOut {
     uint32_t *tiles;     // [3 * max_tiles] or null
     uint32_t *n_tiles;   // [1] or null
     int tile_m;          // rows per tile
-    uint32_t *tile_rows; // [max tiles][tile_m] token (pair / k) of each tile row, or null; rows
-                         // past a partial tile's end repeat its last row
+    uint32_t *tile_rows; // [max tiles][tile_m] token (pair / k) of each tile row, or null; the
+                         // entries past a partial tile's rows are left unwritten
 };
 hipError_t launch_topk(const bf16_t *logits, int T, int E, int k, bool norm, bf16_t *gates,
                        uint32_t *ids, bf16_t *scores, hipStream_t stream);
@@ -191,8 +191,8 @@ constexpr int kGemmTileN = 64;
 // null), K % 512 == 0, N a multiple of 128 (glu) or 256. A is packed (launch_apack) with its X
 // splits AX [rows][3][ax_e] (ax_e = K / 64: one entry per group).
 // Routed tiles come from routing.tiles (64 rows); their A rows from tile_rows [tile][64] (token
-// of each tile row, the tile's last row repeated past its rows) or, without tile_rows, the sorted
-// positions themselves. glu: out = packed R(silu(R(A.w0)) * R(A.w1)) and OX [rows][3][N / 64]
+// of each tile row; only the tile's rows are read, rows past them repeat its last one) or,
+// without tile_rows, the sorted positions themselves. glu: out = packed R(silu(R(A.w0)) * R(A.w1)) and OX [rows][3][N / 64]
 // the X splits of each output row's groups; else out = R(A.w0). The shared product (sh)
 // has the same K and N and comes first.
 struct MoeGemmJob {

@@ -26,14 +26,17 @@ __device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *tmp, uint32_t *to
     }
     if (lane == 63) tmp[wave] = inc;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t run = 0;
-        for (int w = 0; w < NT / 64; ++w) {
-            uint32_t t = tmp[w];
-            tmp[w] = run;
-            run += t;
+    if (wave == 0) {  // the wave totals' exclusive scan, lane w holding wave w
+        constexpr int NWV = NT / 64;
+        const uint32_t t = lane < NWV ? tmp[lane] : 0u;
+        uint32_t s = t;
+#pragma unroll
+        for (int d = 1; d < NWV; d <<= 1) {
+            const uint32_t o = (uint32_t)__shfl_up((int)s, d, 64);
+            if (lane >= d) s += o;
         }
-        tmp[NT / 64] = run;
+        if (lane < NWV) tmp[lane] = s - t;
+        if (lane == NWV - 1) tmp[NWV] = s;
     }
     __syncthreads();
     uint32_t ex = tmp[wave] + inc - v;
@@ -147,12 +150,9 @@ __global__ __launch_bounds__(1024) void route_scatter_kernel(const uint32_t *__r
         if (o.order) o.order[pos] = p;
         if (o.inverse) o.inverse[p] = pos;
         if (o.token) o.token[pos] = p / (uint32_t)k;
-        if (o.tile_rows) {  // the token of each tile row; a partial tile repeats its last row
+        if (o.tile_rows) {  // the token of each tile row (rows past a partial tile's are not written)
             const uint32_t in_e = pos - eoff[my_e];
-            uint32_t *tr = o.tile_rows + (size_t)(tbase[my_e] + in_e / m) * m;
-            tr[in_e % m] = p / (uint32_t)k;
-            if (in_e + 1 == ecnt[my_e])
-                for (uint32_t rr = in_e % m + 1; rr < m; ++rr) tr[rr] = p / (uint32_t)k;
+            o.tile_rows[(size_t)(tbase[my_e] + in_e / m) * m + in_e % m] = p / (uint32_t)k;
         }
     }
     if (b != 0) return;
