@@ -151,26 +151,33 @@ def time_stages(dev, x, reps: int, torch):
 
 
 def time_gateup_kernel(dev, x, reps: int, torch, cold=None) -> float:
-    """Mean duration of the decode gate/up kernel in microseconds: events updated by its own launch
-    at the kernel's start and end (mrun_moe_forward_timed, hipExtLaunchKernel), one pair per
-    forward, on the launch stream; no launch gap is included. With `cold` (a ColdTimer) the
-    last-level cache is flushed before every forward (outside the kernel's events)."""
+    """Mean duration of the decode gate/up kernel in microseconds, one forward after another on
+    the stream: mrun_moe_forward_timed has the kernel stamp the device wall clock at its
+    workgroups' starts and its waves' ends (64 folded pairs per forward); the span from the first
+    start to the last end has no launch gap and no dispatch latency. With `cold` (a ColdTimer) the last-level cache is flushed before every forward."""
     from mrun_amd import _lib
     lib = _lib.load()
+    hz = lib.mrun_wall_clock_hz()
+    if hz <= 0:
+        raise RuntimeError("the device does not report its wall clock rate")
     T = x.shape[0]
-    ev = Events(2 * reps)
     stream = torch.cuda.current_stream()
     out = torch.empty_like(x)
     ws = dev.workspace(T)
+    clock = torch.zeros(reps, 64, 2, dtype=torch.int64, device=x.device)
+    clock[:, :, 0] = -1  # 64 pairs (UINT64_MAX, 0) per forward: the kernel lowers and raises them
     for r in range(reps):
         if cold is not None:
             cold.flush(stream)
         _lib.check(lib.mrun_moe_forward_timed(
             ctypes.byref(dev.c), ctypes.c_void_p(x.data_ptr()), T, ctypes.c_void_p(out.data_ptr()),
             ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(stream.cuda_stream),
-            ctypes.c_void_p(ev.ev[2 * r]), ctypes.c_void_p(ev.ev[2 * r + 1])))
+            ctypes.c_void_p(clock[r].data_ptr())))
     torch.cuda.synchronize()
-    return float(np.mean([ev.ms(2 * r, 2 * r + 1) for r in range(1, reps)]) * 1e3)
+    c = clock.cpu().numpy().view(np.uint64)
+    ticks = (c[1:, :, 1].max(axis=1) - c[1:, :, 0].min(axis=1)).astype(np.float64)  # (the first
+    # forward is a warm-up)
+    return float(np.mean(ticks) / hz * 1e6)
 
 
 def time_graph(dev, x, steps: int, torch, per_graph: int = 1):
@@ -643,9 +650,9 @@ def main(argv=None) -> int:
                 "frac_cold": gbytes / (gu_us_cold * 1e-6) / HBM_PEAK if gu_us_cold else None,
                 "bytes_per_launch": gbytes, "us_per_launch": gu_us,
                 "us_per_launch_cold": gu_us_cold, "us_per_launch_with_gap": gu_stage_us,
-                "timing": "HIP events recorded by the launch itself at the kernel's start and end "
-                          "(hipExtLaunchKernel) on its stream, mean of 99 forwards (29 cold); "
-                          "us_per_launch_with_gap: events between launches"}
+                "timing": "the kernel's own device wall-clock stamps (s_memrealtime) at its first "
+                          "wave's start and last wave's end (mrun_moe_forward_timed), mean of 99 "
+                          "forwards (29 cold); us_per_launch_with_gap: HIP events between launches"}
 
     sweep = []
     if not args.no_sweep:

@@ -148,9 +148,10 @@ extern "C" {
         workspace: *mut c_void,
         workspace_bytes: usize,
         stream: mrun_stream_t,
-        start_event: *mut c_void,
-        stop_event: *mut c_void,
+        clock: *mut u64,
     ) -> c_int;
+    /// Ticks per second of the clock `mrun_moe_forward_timed` reads (instrumentation).
+    pub fn mrun_wall_clock_hz() -> i64;
     /// Byte offsets of the last forward's routing inside its workspace (instrumentation).
     pub fn mrun_moe_workspace_routing(cfg: *const mrun_moe_config, tokens: i32, at: *mut usize)
         -> c_int;

@@ -124,15 +124,20 @@ int mrun_moe_forward_profiled(const mrun_sparse_moe *moe, const mrun_bf16 *x, in
                               int32_t *n_stages);
 const char *mrun_moe_stage_names(const mrun_moe_config *cfg, int32_t tokens);
 
-/* mrun_moe_forward with the decode gate/up kernel timed by its own launch (benchmark
- * instrumentation; no counterpart in the reference): start_event and stop_event, hipEvent_t
- * handles created by the caller, are updated by that launch at the kernel's start and end
- * (hipExtLaunchKernel), so their elapsed time is the kernel's duration without launch gaps. A
- * batch that runs the prefill schedule has no such launch: the call returns MRUN_ERR_UNSUPPORTED
- * and enqueues nothing. */
+/* mrun_moe_forward with the decode gate/up kernel timed from inside (benchmark instrumentation;
+ * no counterpart in the reference): clock is a device buffer of 64 u64 pairs that the caller sets
+ * to (UINT64_MAX, 0) beforehand; workgroup i of the kernel lowers pair i % 64's first value to
+ * its start and raises its second to its waves' ends, in ticks of the device's constant wall
+ * clock (mrun_wall_clock_hz). The largest second value minus the smallest first one is the
+ * kernel's duration without launch gaps or dispatch latency. A batch that runs the prefill
+ * schedule has no such kernel: the call returns MRUN_ERR_UNSUPPORTED and enqueues nothing. */
 int mrun_moe_forward_timed(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t tokens,
                            mrun_bf16 *out, void *workspace, size_t workspace_bytes,
-                           mrun_stream_t stream, void *start_event, void *stop_event);
+                           mrun_stream_t stream, uint64_t *clock);
+
+/* Ticks per second of the wall clock mrun_moe_forward_timed reads, on the current device; -1 if
+ * the runtime does not report it. */
+int64_t mrun_wall_clock_hz(void);
 
 /* Where a forward leaves its routing inside the caller's workspace (instrumentation for tests and
  * profilers; no counterpart in the reference, whose intermediate arrays are not observable). For

@@ -89,8 +89,9 @@ SIGNATURES = {
     "mrun_moe_forward_timed": (
         c_int32,
         [POINTER(SparseMoe), c_void_p, c_int32, c_void_p, c_void_p, c_size_t, c_void_p,
-         c_void_p, c_void_p],
+         c_void_p],
     ),
+    "mrun_wall_clock_hz": (c_int64, []),
     "mrun_moe_router": (
         c_int32,
         [POINTER(SparseMoe), c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p,

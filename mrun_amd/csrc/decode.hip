@@ -509,6 +509,17 @@ __attribute__((amdgpu_waves_per_eu(LOOP && CPL == 3 ? 3 : 1))) void decode_gateu
         q.bits = sh ? a.bits : b.bits;
         return q;
     };
+    // benchmark instrumentation (j.clock set): the device wall clock at each workgroup's start and
+    // at each wave's end, whichever way the wave leaves, folded into pair blockIdx % 64 of the 64
+    // (start min, end max) pairs (one address for every workgroup serialises its atomics)
+    unsigned long long *const clk = j.clock ? j.clock + 2 * (blockIdx.x & 63) : nullptr;
+    struct ClockEnd {
+        unsigned long long *c;
+        __device__ ~ClockEnd() {
+            if (c && (threadIdx.x & 63) == 0) atomicMax(c + 1, __builtin_amdgcn_s_memrealtime());
+        }
+    } clock_end{clk};
+    if (clk && threadIdx.x == 0) atomicMin(clk, __builtin_amdgcn_s_memrealtime());
     const QW w0 = pick(j.sg, j.wg), w1 = pick(j.su, j.wu);
     int e = 0, rb, a_div, ldo;
     uint64_t pm0, pm1;
@@ -793,14 +804,8 @@ static void launch_k3_pb(const DecodeJob &j, hipStream_t s);
 // row blocks at T = 1 to 16; caps of 512, 2048 and 4096 per token measured slower.) Narrower rows
 // (one round already) take one row block per workgroup (the loop measured slower there).
 template <int RG, int NW, bool LOOP>
-static void launch_k2_l(const DecodeJob &j, int n_ch, dim3 g2, hipStream_t s,
-                        const StageMarks *marks) {
-    auto go1 = [&](auto kernel) {
-        if (marks && marks->k2_start)  // timed by the launch itself (benchmark instrumentation)
-            hipExtLaunchKernelGGL(kernel, g2, dim3(64 * NW), 0, s, marks->k2_start, marks->k2_stop,
-                                  0, j);
-        else kernel<<<g2, 64 * NW, 0, s>>>(j);
-    };
+static void launch_k2_l(const DecodeJob &j, int n_ch, dim3 g2, hipStream_t s) {
+    auto go1 = [&](auto kernel) { kernel<<<g2, 64 * NW, 0, s>>>(j); };
     // the shared expert's workgroups last at T <= 2 (T = 1: 14.9 -> 14.2 us per block, T = 2:
     // 20.8 -> 19.3), first above (last measured 4 and 7 us slower at T = 4 and 16)
     auto go = [&](auto first, auto last) {
@@ -814,7 +819,7 @@ static void launch_k2_l(const DecodeJob &j, int n_ch, dim3 g2, hipStream_t s,
 }
 
 template <int RG, int NW>
-static void launch_k2(DecodeJob j, int n_ch, hipStream_t s, const StageMarks *marks) {
+static void launch_k2(DecodeJob j, int n_ch, hipStream_t s) {
     const int per_slot = j.I / (NW * RG), sh_blocks = j.S / (NW * RG);
     int L = 1;
     while (RG == 1 && n_ch > 64 && j.max_slots * per_slot / L > 1024 * j.T &&
@@ -822,8 +827,8 @@ static void launch_k2(DecodeJob j, int n_ch, hipStream_t s, const StageMarks *ma
         L *= 2;
     j.gu_loop = L;
     dim3 g2(shared_gateup_blocks(j, NW * RG * L) + (j.I / (NW * RG * L)) * j.max_slots);
-    if (RG == 1 && L > 1) launch_k2_l<1, NW, true>(j, n_ch, g2, s, marks);
-    else launch_k2_l<RG, NW, false>(j, n_ch, g2, s, marks);
+    if (RG == 1 && L > 1) launch_k2_l<1, NW, true>(j, n_ch, g2, s);
+    else launch_k2_l<RG, NW, false>(j, n_ch, g2, s);
 }
 
 template <int LPR, int CPL>
@@ -877,9 +882,9 @@ hipError_t launch_decode(const DecodeJob &j, hipStream_t s, StageMarks *marks) {
     // wider than 2048 take one row per wave and the streaming loop at every T
     const int rg = n_ch > 64 ? 1 : (j.T <= 2 ? 2 : 4);
     // 4 waves per workgroup: 8 and 16 (fewer redundant top-ks per CU) measured slower
-    if (rg == 1) launch_k2<1, 4>(j, n_ch, s, marks);
-    else if (rg == 2) launch_k2<2, 4>(j, n_ch, s, marks);
-    else launch_k2<4, 4>(j, n_ch, s, marks);
+    if (rg == 1) launch_k2<1, 4>(j, n_ch, s);
+    else if (rg == 2) launch_k2<2, 4>(j, n_ch, s);
+    else launch_k2<4, 4>(j, n_ch, s);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (marks) marks->mark(s);

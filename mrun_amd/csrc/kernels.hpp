@@ -34,9 +34,10 @@ struct StageMarks {
     hipEvent_t *events = nullptr;
     int n_events = 0;
     int count = 0;
-    // optional: the decode gate/up launch records these itself at its start and end
-    // (hipExtLaunchKernel), so their elapsed time is that kernel's duration
-    hipEvent_t k2_start = nullptr, k2_stop = nullptr;
+    // optional: 64 (start, end) pairs; the decode gate/up kernel lowers start to its workgroups'
+    // starts and raises end to their waves' ends (workgroup i in pair i % 64), in ticks of the
+    // device wall clock (s_memrealtime)
+    unsigned long long *k2_clock = nullptr;
     void mark(hipStream_t s) {
         if (events && count + 1 < n_events) (void)hipEventRecord(events[count + 1], s);
         ++count;
@@ -144,6 +145,7 @@ struct DecodeJob {
     // out = R(residual + block output) (out may alias residual).
     const bf16_t *norm_src, *norm_w, *residual;
     float eps;
+    unsigned long long *clock;  // benchmark instrumentation (StageMarks::k2_clock), or null
 };
 bool decode_supported(int D, int I, int S, int T, int k, int E);
 hipError_t launch_decode(const DecodeJob &job, hipStream_t stream, StageMarks *marks);

@@ -416,6 +416,7 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
             if (S) TRY(tensor::linear(x, T, m.shared_expert_gate, sh_logit, s));
             j.router_done = 1;
         }
+        j.clock = st.k2_clock;
         TRY_HIP(launch_decode(j, s, &st), "decode");
         return Ok();
     }
@@ -698,7 +699,7 @@ int mrun_moe_forward_profiled(const mrun_sparse_moe *moe, const mrun_bf16 *x, in
 
 int mrun_moe_forward_timed(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t tokens,
                            mrun_bf16 *out, void *workspace, size_t workspace_bytes,
-                           mrun_stream_t stream, void *start_event, void *stop_event) {
+                           mrun_stream_t stream, uint64_t *clock) {
     Status st = check_block(moe);
     if (st.ok() && tokens < 0) st = Err(MRUN_ERR_INVALID, "tokens must not be negative");
     if (st.ok() && tokens == 0) return report(st);  // an empty batch: nothing to do
@@ -706,18 +707,25 @@ int mrun_moe_forward_timed(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32
     if (st.ok()) st = check_ptr(out, "out");
     if (st.ok()) st = check_ptr(workspace, "workspace");
     if (st.ok() && x == out) st = Err(MRUN_ERR_INVALID, "out must not alias x");
-    if (st.ok() && (!start_event || !stop_event))
-        st = Err(MRUN_ERR_INVALID, "forward_timed needs both events");
+    if (st.ok()) st = check_ptr(clock, "clock");
     if (st.ok() && !models::is_decode(*moe, tokens))
         st = Err(MRUN_ERR_UNSUPPORTED,
                  "forward_timed: this batch runs the prefill schedule, which has no decode "
                  "gate/up launch to time");
     StageMarks marks;
-    marks.k2_start = (hipEvent_t)start_event, marks.k2_stop = (hipEvent_t)stop_event;
+    marks.k2_clock = (unsigned long long *)clock;
     if (st.ok())
         st = models::sparse_moe_forward(*moe, x, tokens, out, (char *)workspace, workspace_bytes,
                                         (hipStream_t)stream, &marks);
     return report(st);
+}
+
+int64_t mrun_wall_clock_hz(void) {
+    int dev = 0, khz = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz <= 0)
+        return -1;
+    return (int64_t)khz * 1000;
 }
 
 const char *mrun_moe_stage_names(const mrun_moe_config *cfg, int32_t tokens) {

@@ -273,23 +273,33 @@ def test_empty_batch(q_dev):
 
 def test_timed_forward_matches_forward(q_dev):
     """mrun_moe_forward_timed (the benchmark's kernel-timed forward) gives the plain forward's bits,
-    and its events bracket the decode gate/up kernel: a positive duration below the forward's."""
+    and its wall-clock stamps bracket the decode gate/up kernel: a positive duration, below the
+    span of HIP events around the whole forward."""
     import bench
     from mrun_amd import _lib
 
+    lib = _lib.load()
+    hz = lib.mrun_wall_clock_hz()
+    assert hz > 0
     x = M.bf16_tensor(synth.make_x(Q, 1, config=synth.CFG_DECODE, layer=11))
     ref = M.bf16_bits(q_dev.forward(x))
     out = torch.empty_like(x)
     ws = q_dev.workspace(1)
+    clock = torch.zeros(64, 2, dtype=torch.int64, device="cuda")
+    clock[:, 0] = -1  # 64 pairs (UINT64_MAX, 0)
     ev = bench.Events(2)
     stream = torch.cuda.current_stream()
-    _lib.check(_lib.load().mrun_moe_forward_timed(
+    ev.record(0, stream)
+    _lib.check(lib.mrun_moe_forward_timed(
         ctypes.byref(q_dev.c), ctypes.c_void_p(x.data_ptr()), 1, ctypes.c_void_p(out.data_ptr()),
         ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(stream.cuda_stream),
-        ctypes.c_void_p(ev.ev[0]), ctypes.c_void_p(ev.ev[1])))
+        ctypes.c_void_p(clock.data_ptr())))
+    ev.record(1, stream)
     torch.cuda.synchronize()
     assert np.array_equal(M.bf16_bits(out), ref)
-    assert 0.0 < ev.ms(0, 1) < 1.0  # milliseconds
+    c = clock.cpu().numpy().view(np.uint64)
+    kernel_ms = float(c[:, 1].max() - c[:, 0].min()) / hz * 1e3
+    assert 0.0 < kernel_ms < ev.ms(0, 1) < 1.0, (kernel_ms, ev.ms(0, 1))
 
 
 def test_forward_is_deterministic(q_dev):

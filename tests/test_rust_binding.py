@@ -13,7 +13,8 @@ RUST = ROOT / "bindings" / "rust" / "src" / "lib.rs"
 
 # C scalar type -> the Rust type the binding must use
 C_SCALARS = {
-    "int": "c_int", "int32_t": "i32", "int64_t": "i64", "uint32_t": "u32", "size_t": "usize",
+    "int": "c_int", "int32_t": "i32", "int64_t": "i64", "uint32_t": "u32", "uint64_t": "u64",
+    "size_t": "usize",
     "float": "f32", "char": "c_char", "void": "c_void", "uint16_t": "u16",
     "mrun_bf16": "mrun_bf16", "mrun_stream_t": "mrun_stream_t", "mrun_quantized": "mrun_quantized",
     "mrun_linear": "mrun_linear", "mrun_moe_config": "mrun_moe_config",
