@@ -260,12 +260,14 @@ hipError_t launch_rows(const bf16_t *x, int T, int D, const bf16_t *W, const bf1
 // nuvec.rs:1173-1204) and dotted in f32. Lane l owns the 8-element chunks [8l + 512i, +8) of each
 // 2048-wide pass (a chunk lies in one group); all of a pass's loads are issued before any is used.
 template <int MAXT>
-__device__ __forceinline__ void qrouter_row(const bf16_t *x, int T, int D, const QW &w, int row,
+__device__ __forceinline__ void qrouter_row(const bf16_t *x, int T, int D, const QW w, int row,
                                             const bf16_t *bias, bf16_t *out, int ldo, int lane) {
     float acc[MAXT];
 #pragma unroll
     for (int t = 0; t < MAXT; ++t) acc[t] = 0.f;
-    const int groups = D / w.group, wpr = D * w.bits / 32;  // code words per row
+    // group sizes are powers of two (32, 64 or 128): a shift, not a division per chunk
+    const int gshift = __builtin_ctz((unsigned)w.group);
+    const int groups = D >> gshift, wpr = D * w.bits / 32;  // code words per row
     const uint32_t *codes = w.codes + (size_t)row * wpr;
     const bf16_t *sc = w.scales + (size_t)row * groups;
     const bf16_t *bi = w.biases ? w.biases + (size_t)row * groups : nullptr;
@@ -277,8 +279,8 @@ __device__ __forceinline__ void qrouter_row(const bf16_t *x, int T, int D, const
             const int d = min(d0 + 512 * i, D - 8);  // clamped; chunks past D are not used
             if (w.bits == 8) cw[i] = *(const uint2 *)(codes + d / 4);
             else cw[i] = make_uint2(codes[d / 8], 0u);
-            sraw[i] = sc[d / w.group];
-            braw[i] = bi ? bi[d / w.group] : 0u;
+            sraw[i] = sc[d >> gshift];
+            braw[i] = bi ? bi[d >> gshift] : 0u;
         }
         float wv[4][8];
 #pragma unroll
@@ -333,22 +335,25 @@ __device__ __forceinline__ void qrouter_row(const bf16_t *x, int T, int D, const
 // registers and schedule)
 template <int MAXT, bool NORM, bool QUANT>
 __global__ __launch_bounds__(256) void decode_router_kernel(DecodeJob j) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // the wave index in a scalar register: the row, its weights and the branches below are the
+    // wave's own (per-lane values would make every field of a quantized row a per-lane load)
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = blockIdx.x * 4 + wave;
     const int D = j.D;
     const bf16_t *w = nullptr, *bias = nullptr;
-    const QW *qw = nullptr;  // a quantized row instead (row qr of it)
+    bool quant = false;  // a quantized row instead (row qr of qw)
+    QW qw{};
     int qr = 0;
     bf16_t *out = nullptr;
     int ldo = 1;
     if (r < j.E) {
         if (!QUANT || j.router) w = j.router + (size_t)r * D;
-        else qw = &j.router_q, qr = r;
+        else quant = true, qw = j.router_q, qr = r;
         out = j.logits + r, ldo = j.E;
         bias = j.router_bias ? j.router_bias + r : nullptr;
     } else if (r == j.E && j.S) {
         if (!QUANT || j.sh_gate_w) w = j.sh_gate_w;
-        else qw = &j.sh_gate_q;
+        else quant = true, qw = j.sh_gate_q;
         bias = j.sh_gate_b, out = j.sh_logit;
     }
     // the weight row's first pass is loaded before anything waits (the norm below, in particular)
@@ -399,7 +404,7 @@ __global__ __launch_bounds__(256) void decode_router_kernel(DecodeJob j) {
         x = hs;
     }
     if (w) router_row<MAXT>(x, j.T, D, w, first, bias, out, ldo, lane);
-    else if (QUANT && qw) qrouter_row<MAXT>(x, j.T, D, *qw, qr, bias, out, ldo, lane);
+    else if (QUANT && quant) qrouter_row<MAXT>(x, j.T, D, qw, qr, bias, out, ldo, lane);
 }
 
 // ---------------------------------------------------------------------------------------------
