@@ -93,7 +93,8 @@ template <int CPL>
 __device__ __forceinline__ void load_wrow(const QW &w, int e, int row, int li, int lpr,
                                           WRow<CPL> &r) {
     const int n_ch = w.in >> 5;
-    const int groups = w.in / w.group;
+    const int gshift = __builtin_ctz((unsigned)w.group);  // groups of 32, 64 or 128
+    const int groups = w.in >> gshift;
     const size_t rr = (size_t)e * w.out + min(row, w.out - 1);
     const uint32_t *codes = w.codes + rr * (size_t)(w.in >> 3);
     // without biases the scales stand in, so the load is unconditional; row_part zeroes the term
@@ -104,7 +105,7 @@ __device__ __forceinline__ void load_wrow(const QW &w, int e, int row, int li, i
         const int ch = li + c * lpr;
         const int chc = min(ch, n_ch - 1);
         r.q[c] = *(const uint4 *)(codes + (size_t)chc * 4);
-        const size_t gi = rr * groups + (chc * 32) / w.group;
+        const size_t gi = rr * groups + ((chc * 32) >> gshift);
         r.s[c] = w.scales[gi];
         r.b[c] = biases[gi];
         r.ok |= (row < w.out && ch < n_ch) ? (1u << c) : 0u;

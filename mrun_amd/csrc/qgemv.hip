@@ -98,8 +98,9 @@ __device__ __forceinline__ Chunk load_chunk(const QW &w, int e, int row, int ch)
         c.s = 1.f, c.b = 0.f;
         return c;
     }
-    const int groups = w.in / w.group;
-    const int g = (ch * CPC) / w.group;
+    const int gshift = __builtin_ctz((unsigned)w.group);  // groups of 32, 64 or 128
+    const int groups = w.in >> gshift;
+    const int g = (ch * CPC) >> gshift;
     c.s = bf2f(w.scales[r * groups + g]);
     c.b = w.biases ? bf2f(w.biases[r * groups + g]) : 0.f;
     return c;
