@@ -54,6 +54,21 @@ __device__ __forceinline__ float lane_f32(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// v + (a row broadcast of v) in some rows; the other rows keep v. One v_add_f32 with the DPP
+// control (the DPP source is the first operand; disabled rows leave the destination, which is v).
+// The s_nops cover the DPP read of a just-written VGPR and a read of the result right after.
+//   bcast15: rows 1 and 3 add lanes 15 and 47;  bcast31: rows 2 and 3 add lane 31.
+__device__ __forceinline__ float add_row_bcast15(float v) {
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %0, %0 row_bcast:15 row_mask:0xa bank_mask:0xf\n\ts_nop 1"
+        : "+v"(v));
+    return v;
+}
+__device__ __forceinline__ float add_row_bcast31(float v) {
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %0, %0 row_bcast:31 row_mask:0xc bank_mask:0xf\n\ts_nop 1"
+        : "+v"(v));
+    return v;
+}
+
 __device__ __forceinline__ float row_sum16(float v) {
     v += dpp_f32<0xB1>(v);
     v += dpp_f32<0x4E>(v);
@@ -82,10 +97,14 @@ __device__ __forceinline__ float group_sum(float v) {
     }
     v = row_sum16(v);
     if (WIDTH == 16) return v;
-    const float r0 = lane_f32(v, 0), r1 = lane_f32(v, 16), r2 = lane_f32(v, 32),
-                r3 = lane_f32(v, 48);
-    if (WIDTH == 32) return (threadIdx.x & 32) ? r2 + r3 : r0 + r1;
-    return (r0 + r1) + (r2 + r3);
+    // row totals r0..r3 -> (r0 + r1) and (r2 + r3) in rows 1 and 3 (row_bcast:15 adds lane 15's
+    // value into row 1 and lane 47's into row 3; the other rows keep theirs), then
+    // (r0 + r1) + (r2 + r3) in row 3 (row_bcast:31 adds lane 31's value into rows 2 and 3).
+    // Addition commutes exactly, so the sums are bit for bit those of (r0 + r1) + (r2 + r3).
+    v = add_row_bcast15(v);
+    if (WIDTH == 32) return (threadIdx.x & 32) ? lane_f32(v, 63) : lane_f32(v, 31);
+    v = add_row_bcast31(v);
+    return lane_f32(v, 63);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
