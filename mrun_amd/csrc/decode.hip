@@ -10,7 +10,8 @@
 //                expert's gate/up rows for its pairs. The first routed workgroup publishes the
 //                routing for K3.
 //   K3 down    : prefetches the shared expert's down rows, reads the routing, computes the routed
-//                down rows of every active expert for its 4 or 8 output rows, then the combine:
+//                down rows of every active expert for its 4 or 8 output rows and its group of
+//                tokens (two groups from T = 2), then the combine of those tokens:
 //                out = R(R(sum_j R(y[t,j] * s[t,j])) + R(R(sigmoid(g_t)) * shared[t])).
 // Rows wider than 2048 (the Coder shape): a K2 workgroup streams several row blocks pair by pair
 // with the next rows loaded before the current ones are computed, and without a shared expert K3
@@ -596,7 +597,11 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeJob j) {
     __shared__ float ysh[kMaxT][kDownRowsPerWG];
     __shared__ bf16_t shl[kMaxT];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int d0 = blockIdx.x * kDownRowsPerWG;
+    // workgroup = (token group, row block); the token group's pairs are a contiguous range, and a
+    // token's combine needs only its own pairs
+    const int n_rb = j.D / kDownRowsPerWG;
+    const int d0 = (blockIdx.x % n_rb) * kDownRowsPerWG;
+    const int t0 = (blockIdx.x / n_rb) * j.down_tokens, t1 = min(j.T, t0 + j.down_tokens);
 
     // the routing is loaded first (loads complete in issue order), then what does not depend on
     // it: the shared expert's rows and first activation row, the shared gate logits, this wave's
@@ -625,15 +630,16 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeJob j) {
             const int g = wave + 4 * i;
             load_wrow<SCPL>(sd, 0, g < SNRG ? d0 + g * SRPI + lane / SLPR : j.D, sli, SLPR, sr[i]);
         }
-        load_xrow_raw<SCPL>(has_s ? j.sh_act : j.act, sli, SLPR, (has_s ? j.S : j.I) >> 5, scur);
+        load_xrow_raw<SCPL>(has_s ? j.sh_act + (size_t)t0 * j.S : j.act, sli, SLPR,
+                            (has_s ? j.S : j.I) >> 5, scur);
     }
     // clamped indices and unconditional LDS writes (threads past the end repeat the last value):
     // a load used under a condition would make the wait there cover every load issued before
     const bf16_t *shl_src = j.S ? j.sh_logit : j.scores;  // any valid pointer without a shared expert
     const uint32_t my_shl = shl_src[min((int)threadIdx.x, j.T - 1)];
     const int li = lane % LPR, rsub = lane / LPR;
-    const int per_wave = (P + 3) / 4;
-    const int p_lo = wave * per_wave, p_hi = min(P, p_lo + per_wave);
+    const int per_wave = ((t1 - t0) * j.k + 3) / 4;
+    const int p_lo = t0 * j.k + wave * per_wave, p_hi = min(t1 * j.k, p_lo + per_wave);
     XRaw xr[PB][CPL];
     auto load_act = [&](int pb) {  // rows clamped into [0, P): also a wave without pairs loads
 #pragma unroll
@@ -675,8 +681,8 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeJob j) {
     }
     if (j.S) {
         XRaw nxt[SCPL];
-        for (int t = 0; t < j.T; ++t) {
-            load_xrow_raw<SCPL>(j.sh_act + (size_t)min(t + 1, j.T - 1) * j.S, sli, SLPR, j.S >> 5,
+        for (int t = t0; t < t1; ++t) {
+            load_xrow_raw<SCPL>(j.sh_act + (size_t)min(t + 1, t1 - 1) * j.S, sli, SLPR, j.S >> 5,
                                 nxt);
             XChunk xc[SCPL];
             pair_xrow<SCPL>(scur, xc);
@@ -693,8 +699,8 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeJob j) {
     }
     shl[min((int)threadIdx.x, kMaxT - 1)] = (bf16_t)my_shl;
     __syncthreads();
-    for (int i = threadIdx.x; i < j.T * kDownRowsPerWG; i += 256) {
-        const int t = i / kDownRowsPerWG, dd = i % kDownRowsPerWG;
+    for (int i = threadIdx.x; i < (t1 - t0) * kDownRowsPerWG; i += 256) {
+        const int t = t0 + i / kDownRowsPerWG, dd = i % kDownRowsPerWG;
         float acc = 0.f;
         for (int jj = 0; jj < j.k; ++jj) {
             const int p = t * j.k + jj;
@@ -801,6 +807,12 @@ static void launch_k1(const DecodeJob &j, hipStream_t s) {
 template <int LPR, int CPL, int PB, int DR>
 static void launch_k3_pb(const DecodeJob &j, hipStream_t s);
 
+// K3 token groups: from T = 2 the tokens are split into two groups, each with its own workgroups
+// for every row block (twice the workgroups, half the pairs each, so each wave's chain of pair
+// batches is half as long). The split keeps every row's bits. T = 16 71.7 -> 66.7 us per block,
+// T = 4 28.3 -> 27.5, T = 2 18.8 -> 18.5; four groups at T = 16 measured 68.4.
+static int k3_token_groups(int T) { return T >= 2 ? 2 : 1; }
+
 // K2 with RG rows per wave and NW waves per workgroup (I and S multiples of NW * RG). With rows
 // wider than 2048 (one row per wave), each workgroup streams gu_loop row blocks, the smallest
 // power of two that keeps the routed workgroups at 1024 per token or fewer (I and S multiples of
@@ -837,7 +849,8 @@ static void launch_k2(DecodeJob j, int n_ch, hipStream_t s) {
 }
 
 template <int LPR, int CPL>
-static void launch_k3_s(const DecodeJob &j, hipStream_t s) {
+static void launch_k3_s(DecodeJob j, hipStream_t s) {
+    j.down_tokens = (j.T + k3_token_groups(j.T) - 1) / k3_token_groups(j.T);
     // output rows per workgroup: two row groups per wave, at least 4 rows (8 with 16-lane rows,
     // where 4, 16 and 32 measured slower: T = 1 18.3, 18.1, 20.7 against 17.4 us per block; fewer
     // workgroups re-read the pairs' activation rows fewer times, until each wave's chain of pair
@@ -847,13 +860,13 @@ static void launch_k3_s(const DecodeJob &j, hipStream_t s) {
     constexpr int DR = 2 * (64 / LPR) > 4 ? 2 * (64 / LPR) : 4;
     constexpr int NRG = DR / (64 / LPR) > 0 ? DR / (64 / LPR) : 1;
     constexpr int PB = (NRG * CPL <= 2) ? 4 : (NRG * CPL <= 4 ? 2 : 1);
-    if (PB == 4 && (j.T * j.k + 3) / 4 <= 2) launch_k3_pb<LPR, CPL, 2, DR>(j, s);
+    if (PB == 4 && (j.down_tokens * j.k + 3) / 4 <= 2) launch_k3_pb<LPR, CPL, 2, DR>(j, s);
     else launch_k3_pb<LPR, CPL, PB, DR>(j, s);
 }
 
 template <int LPR, int CPL, int PB, int DR>
 static void launch_k3_pb(const DecodeJob &j, hipStream_t s) {
-    dim3 grid(j.D / DR);
+    dim3 grid(j.D / DR * ((j.T + j.down_tokens - 1) / j.down_tokens));
     const int sch = j.S ? j.S >> 5 : 16;
     if (sch == 16) decode_down_kernel<LPR, CPL, 16, 1, PB, DR><<<grid, 256, 0, s>>>(j);
     else if (sch < 64) decode_down_kernel<LPR, CPL, 32, 2, PB, DR><<<grid, 256, 0, s>>>(j);

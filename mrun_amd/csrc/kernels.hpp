@@ -134,6 +134,7 @@ struct DecodeJob {
     int topk_in_kernel;  // T <= 4: each workgroup re-derives the top-k from the logits instead
     int router_done;     // logits and sh_logit already computed (quantized router or gate)
     int gu_loop;         // row blocks per K2 workgroup (set by the launcher)
+    int down_tokens;     // tokens per K3 workgroup (set by the launcher)
     bf16_t *sh_logit; // [T]
     bf16_t *sh_act;   // [T, S]
     bf16_t *act;      // [T*k, I], pair p = t*k + j
