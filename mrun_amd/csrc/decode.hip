@@ -855,12 +855,13 @@ static void launch_k3_s(DecodeJob j, hipStream_t s) {
     // where 4, 16 and 32 measured slower: T = 1 18.3, 18.1, 20.7 against 17.4 us per block; fewer
     // workgroups re-read the pairs' activation rows fewer times, until each wave's chain of pair
     // batches grows too long). Pairs per load batch keep a batch's activations and weight rows
-    // within ~128 registers, and are no more than a wave's pairs (a wave takes ceil(P / 4) pairs;
-    // slots past them would load their last pair again)
+    // within ~128 registers; batches of 4 only for waves of more than 8 pairs (a wave takes a
+    // quarter of its group's pairs): with 2 to 8 pairs a wave, batches of 2 measured faster
+    // (T = 4, 4 pairs a wave: 27.1 -> 26.75 us per block) and no slower at T = 1 and 8
     constexpr int DR = 2 * (64 / LPR) > 4 ? 2 * (64 / LPR) : 4;
     constexpr int NRG = DR / (64 / LPR) > 0 ? DR / (64 / LPR) : 1;
     constexpr int PB = (NRG * CPL <= 2) ? 4 : (NRG * CPL <= 4 ? 2 : 1);
-    if (PB == 4 && (j.down_tokens * j.k + 3) / 4 <= 2) launch_k3_pb<LPR, CPL, 2, DR>(j, s);
+    if (PB == 4 && (j.down_tokens * j.k + 3) / 4 <= 8) launch_k3_pb<LPR, CPL, 2, DR>(j, s);
     else launch_k3_pb<LPR, CPL, PB, DR>(j, s);
 }
 
