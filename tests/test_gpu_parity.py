@@ -199,7 +199,8 @@ def test_swiglu_combine_norm():
 # ---------------------------------------------------------------------------------------------
 # the block
 
-@pytest.mark.parametrize("T", [1, 2, 4, 16])
+# T = 3 and 5: the down launch's two token groups of unequal size
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 16])
 def test_block_decode_matches_oracle(q_host, q_dev, T):
     x_np = synth.make_x(Q, T, config=synth.CFG_DECODE, layer=T)
     run_block(q_host, q_dev, x_np, f"Q decode T={T}")
