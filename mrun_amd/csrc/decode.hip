@@ -186,7 +186,7 @@ template <int MAXT>
 __device__ __forceinline__ void router_row(const bf16_t *x, int T, int D, const bf16_t *w,
                                            Row4 first, const bf16_t *bias, bf16_t *out, int ldo,
                                            int lane) {
-    constexpr int TG = 4;
+    constexpr int TG = MAXT < 4 ? MAXT : 4;
     float acc[MAXT];
 #pragma unroll
     for (int t = 0; t < MAXT; ++t) acc[t] = 0.f;
@@ -294,24 +294,32 @@ __device__ __forceinline__ void qrouter_row(const bf16_t *x, int T, int D, const
                 wv[i][e] = __builtin_fmaf((float)q, s, b);
             }
         }
+        // tokens in groups of 4 whose activation loads are issued together (one at a time made
+        // every token a round trip: T = 16 took 11 us longer than the dense router)
+        constexpr int TG = MAXT < 4 ? MAXT : 4;
 #pragma unroll
-        for (int t = 0; t < MAXT; ++t) {
-            if (t < T) {
-                uint4 xv[4];
+        for (int t0 = 0; t0 < MAXT; t0 += TG) {
+            if (t0 < T) {
+                uint4 xv[TG][4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    xv[i] = *(const uint4 *)(x + (size_t)t * D + min(d0 + 512 * i, D - 8));
+                for (int tt = 0; tt < TG; ++tt)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    if (d0 + 512 * i < D) {
-                        float xf[8];
-                        unpack8(xv[i], xf);
-                        float a = acc[t];
+                    for (int i = 0; i < 4; ++i)
+                        xv[tt][i] = *(const uint4 *)(x + (size_t)min(t0 + tt, T - 1) * D +
+                                                     min(d0 + 512 * i, D - 8));
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) a = __builtin_fmaf(xf[e], wv[i][e], a);
-                        acc[t] = a;
+                for (int tt = 0; tt < TG; ++tt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if (d0 + 512 * i < D) {
+                            float xf[8];
+                            unpack8(xv[tt][i], xf);
+                            float a = acc[t0 + tt];
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) a = __builtin_fmaf(xf[e], wv[i][e], a);
+                            acc[t0 + tt] = a;
+                        }
                     }
-                }
             }
         }
     }
@@ -884,7 +892,8 @@ bool decode_supported(int D, int I, int S, int T, int k, int E) {
 
 hipError_t launch_decode(const DecodeJob &j, hipStream_t s, StageMarks *marks) {
     if (!j.router_done) {
-        if (j.T <= 4) launch_k1<4>(j, s);
+        if (j.T == 1) launch_k1<1>(j, s);
+        else if (j.T <= 4) launch_k1<4>(j, s);
         else launch_k1<16>(j, s);
     }
     hipError_t e = hipGetLastError();
