@@ -40,16 +40,24 @@ hipError_t launch_swiglu(const bf16_t *g, const bf16_t *u, int64_t n, bf16_t *ou
 // One workgroup per (token, 2048-column slab); thread = 8 columns. All k row indices, then all k
 // rows, are loaded before the first is used (the rows' loads overlap instead of following each
 // other); the sum stays in j order.
-template <int KMAX>
+//
+// POST (rows of at most 2048, one slab): the layer stack's residual add and the next layer's
+// RMSNorm on the combined row, in the order of rms_norm_row_kernel (lane l of that kernel's wave
+// sums chunks l, l + 64, ... in turn: here chunk l + 64 w sits with wave w's lane l, so the waves
+// pass each lane's running sum on through LDS in wave order), so the bits are those of the
+// separate kernel.
+template <int KMAX, bool POST>
 __global__ __launch_bounds__(256) void combine_kernel(const bf16_t *__restrict__ y,
                                                       const uint32_t *__restrict__ inverse,
                                                       const bf16_t *__restrict__ scores, int T,
                                                       int k, int D, const bf16_t *__restrict__ sh_y,
                                                       const bf16_t *__restrict__ sh_logit,
-                                                      bf16_t *__restrict__ out) {
+                                                      bf16_t *__restrict__ out, PostNorm post) {
     const int t = blockIdx.x;
     const int d = (blockIdx.y * 256 + threadIdx.x) * 8;
-    if (d >= D) return;
+    if (!POST && d >= D) return;
+    const bool on = d < D;
+    const int dc = min(d, D - 8);  // clamped (POST: threads past the row keep to the barriers)
     uint32_t row[KMAX];
     uint32_t sraw[KMAX];
 #pragma unroll
@@ -60,10 +68,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const bf16_t *__restrict__
     }
     uint4 yv[KMAX];
 #pragma unroll
-    for (int jj = 0; jj < KMAX; ++jj) yv[jj] = *(const uint4 *)(y + (size_t)row[jj] * D + d);
+    for (int jj = 0; jj < KMAX; ++jj) yv[jj] = *(const uint4 *)(y + (size_t)row[jj] * D + dc);
+    uint4 rv = make_uint4(0u, 0u, 0u, 0u);
+    if (POST) rv = *(const uint4 *)(post.resid + (size_t)t * D + dc);
     const float sg = sh_y ? rbf(sigmoidf_(bf2f(sh_logit[t]))) : 0.f;
     uint4 sv = make_uint4(0, 0, 0, 0);
-    if (sh_y) sv = *(const uint4 *)(sh_y + (size_t)t * D + d);
+    if (sh_y) sv = *(const uint4 *)(sh_y + (size_t)t * D + dc);
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.f;
@@ -87,16 +97,60 @@ __global__ __launch_bounds__(256) void combine_kernel(const bf16_t *__restrict__
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[i] = f2bf(acc[i]);
     }
-    *(uint4 *)(out + (size_t)t * D + d) = make_uint4(o[0] | (o[1] << 16), o[2] | (o[3] << 16),
-                                                     o[4] | (o[5] << 16), o[6] | (o[7] << 16));
+    if (!POST) {
+        *(uint4 *)(out + (size_t)t * D + d) = make_uint4(o[0] | (o[1] << 16), o[2] | (o[3] << 16),
+                                                         o[4] | (o[5] << 16), o[6] | (o[7] << 16));
+        return;
+    }
+    // resid = R(resid + o); the running sum of squares of chunk (lane, wave) continues wave by wave
+    __shared__ float chain[64];
+    __shared__ float inv_s;
+    float f[8];
+    unpack8(rv, f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = rbf(f[i] + bf2f(o[i]));
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int w = 0; w < 4; ++w) {
+        if (wave == w) {
+            float ss = w == 0 ? 0.f : chain[lane];
+            if (on) ss = sumsq8(f, ss);
+            chain[lane] = ss;
+        }
+        __syncthreads();
+    }
+    if (wave == 0) {
+        const float v = group_sum<64>(chain[lane]);
+        if (lane == 0) inv_s = rms_inv_of(v, D, post.eps);
+    }
+    __syncthreads();
+    if (!on) return;
+    const float inv = inv_s;
+    uint32_t hv[8], rn[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float wv = post.w ? bf2f(post.w[d + i]) : 1.0f;
+        hv[i] = f2bf(rbf(f[i] * inv) * wv);
+        rn[i] = f2bf(f[i]);
+    }
+    *(uint4 *)(post.resid + (size_t)t * D + d) = make_uint4(
+        rn[0] | (rn[1] << 16), rn[2] | (rn[3] << 16), rn[4] | (rn[5] << 16), rn[6] | (rn[7] << 16));
+    *(uint4 *)(post.h + (size_t)t * D + d) = make_uint4(
+        hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16));
 }
 
 hipError_t launch_combine(const bf16_t *y, const uint32_t *inverse, const bf16_t *scores, int T,
                           int k, int D, const bf16_t *sh_y, const bf16_t *sh_logit, bf16_t *out,
-                          hipStream_t stream) {
+                          hipStream_t stream, const PostNorm *post) {
     dim3 grid(T, (D + 2047) / 2048);
-    if (k <= 8) combine_kernel<8><<<grid, 256, 0, stream>>>(y, inverse, scores, T, k, D, sh_y, sh_logit, out);
-    else combine_kernel<16><<<grid, 256, 0, stream>>>(y, inverse, scores, T, k, D, sh_y, sh_logit, out);
+    if (post) {
+        if (D > 2048 || D % 8 != 0 || k > 16) return hipErrorInvalidValue;
+        if (k <= 8) combine_kernel<8, true><<<grid, 256, 0, stream>>>(y, inverse, scores, T, k, D, sh_y, sh_logit, out, *post);
+        else combine_kernel<16, true><<<grid, 256, 0, stream>>>(y, inverse, scores, T, k, D, sh_y, sh_logit, out, *post);
+        return hipGetLastError();
+    }
+    const PostNorm none{};
+    if (k <= 8) combine_kernel<8, false><<<grid, 256, 0, stream>>>(y, inverse, scores, T, k, D, sh_y, sh_logit, out, none);
+    else combine_kernel<16, false><<<grid, 256, 0, stream>>>(y, inverse, scores, T, k, D, sh_y, sh_logit, out, none);
     return hipGetLastError();
 }
 

@@ -258,9 +258,19 @@ hipError_t launch_dense_gemm(const DenseJob &job, hipStream_t stream);
 
 hipError_t launch_swiglu(const bf16_t *g, const bf16_t *u, int64_t n, bf16_t *out,
                          hipStream_t stream);
+// The layer stack's step after a block (rows of at most 2048): resid = R(resid + block output),
+// then the next layer's input h = R(R(resid * rsqrt(mean(resid^2) + eps)) * w) (w null: ones),
+// with the bits of launch_rms_norm(resid, block output, w, ...).
+struct PostNorm {
+    bf16_t *resid;
+    const bf16_t *w;
+    float eps;
+    bf16_t *h;
+};
+// post: the combine also takes that step for its rows (then `out` is not written).
 hipError_t launch_combine(const bf16_t *y, const uint32_t *inverse, const bf16_t *scores, int T,
                           int k, int D, const bf16_t *sh_y, const bf16_t *sh_logit, bf16_t *out,
-                          hipStream_t stream);
+                          hipStream_t stream, const PostNorm *post = nullptr);
 hipError_t launch_rms_norm(const bf16_t *x, const bf16_t *res, const bf16_t *w, int rows, int D,
                            float eps, bf16_t *h, bf16_t *y, hipStream_t stream);
 hipError_t launch_rowdot(const bf16_t *x, int T, int D, const bf16_t *W, int N,

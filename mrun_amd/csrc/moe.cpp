@@ -346,9 +346,13 @@ struct FusedNorm {
     float eps;
 };
 
+// post (the layer stack): when the forward ends in the combine launch and its rows are at most
+// 2048 wide, that launch also takes the stack's residual add and next RMSNorm (post_done set, and
+// `out` is not written).
 static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int T, bf16_t *out,
                                  char *ws, size_t ws_bytes, hipStream_t s, Stages *stg = nullptr,
-                                 const FusedNorm *fn = nullptr) {
+                                 const FusedNorm *fn = nullptr, const PostNorm *post = nullptr,
+                                 bool *post_done = nullptr) {
     Stages none;
     Stages &st = stg ? *stg : none;
     if (st.events && st.n_events > 0) (void)hipEventRecord(st.events[0], s);
@@ -568,7 +572,11 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
         st.mark(s);
         st.mark(s);
     }
-    TRY_HIP(launch_combine(y, po.inverse, scores, T, k, D, sh_y, sh_logit, out, s), "combine");
+    const bool fuse_post = post && D <= 2048 && k <= 16;
+    TRY_HIP(launch_combine(y, po.inverse, scores, T, k, D, sh_y, sh_logit, out, s,
+                           fuse_post ? post : nullptr),
+            "combine");
+    if (post_done) *post_done = fuse_post;
     st.mark(s);
     return Ok();
 }
@@ -964,11 +972,17 @@ int mrun_moe_stack_forward(const mrun_sparse_moe *layers, int32_t n_layers,
         if (!fused)
             st = hip_status(launch_rms_norm(x, nullptr, wl(0), tokens, D, eps, nullptr, h, s), "stack norm");
         for (int32_t l = 0; !fused && st.ok() && l < n_layers; ++l) {
-            st = models::sparse_moe_forward(layers[l], h, tokens, o, ws, blk, s);
-            if (!st.ok()) break;
-            // x = R(x + o), and the next layer's input h = rms_norm(x) (the last h is unused)
+            // x = R(x + o), and the next layer's input h = rms_norm(x) (the last h is unused):
+            // inside the block's combine launch when it has one, else a launch of its own
             const bf16_t *w = wl(l + 1 < n_layers ? l + 1 : l);
-            st = hip_status(launch_rms_norm(x, o, w, tokens, D, eps, x, h, s), "stack add_rms_norm");
+            const PostNorm pn{x, w, eps, h};
+            bool done = false;
+            st = models::sparse_moe_forward(layers[l], h, tokens, o, ws, blk, s, nullptr, nullptr,
+                                            &pn, &done);
+            if (!st.ok()) break;
+            if (!done)
+                st = hip_status(launch_rms_norm(x, o, w, tokens, D, eps, x, h, s),
+                                "stack add_rms_norm");
         }
     }
     return report(st);
