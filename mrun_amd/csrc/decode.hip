@@ -91,7 +91,7 @@ __device__ __forceinline__ void gemv_wave(const QW &w0, const QW &w1, int e, int
             const int row = row_base + lane;
             if (lane < RG && row < w0.out) {
                 const float gt = rbf(a0), up = rbf(a1);
-                out[(size_t)p * ldo + row] = (bf16_t)f2bf((gt * sigmoidf_(gt)) * up);
+                out[(size_t)p * ldo + paired_index(row)] = (bf16_t)f2bf((gt * sigmoidf_(gt)) * up);
             }
         } else {
 #pragma unroll
@@ -105,7 +105,7 @@ __device__ __forceinline__ void gemv_wave(const QW &w0, const QW &w1, int e, int
                         const float gt = rbf(a0), up = rbf(a1);
                         v = (gt * sigmoidf_(gt)) * up;
                     }
-                    out[(size_t)p * ldo + row] = (bf16_t)f2bf(v);
+                    out[(size_t)p * ldo + paired_index(row)] = (bf16_t)f2bf(v);
                 }
             }
         }
@@ -134,7 +134,7 @@ __device__ __forceinline__ void gemv_wave_stream1(const QW &w0, const QW &w1, in
         const float a0 = group_sum<64>(row_part(g, xc)), a1 = group_sum<64>(row_part(u, xc));
         if (lane == 0 && row < w0.out) {
             const float gt = rbf(a0), up = rbf(a1);
-            orow[row] = (bf16_t)f2bf((gt * sigmoidf_(gt)) * up);
+            orow[paired_index(row)] = (bf16_t)f2bf((gt * sigmoidf_(gt)) * up);
         }
     };
     int row = row0;
@@ -679,7 +679,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeJob j) {
             const int p = pb + b;
             if (p >= p_hi) break;
             XChunk xc[CPL];
-            pair_xrow<CPL>(xr[b], xc);
+            chunks_of_paired<CPL>(xr[b], xc);
 #pragma unroll
             for (int g = 0; g < NRG; ++g) {
                 const float y = group_sum<LPR>(row_part(wr[b][g], xc));
@@ -693,7 +693,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeJob j) {
             load_xrow_raw<SCPL>(j.sh_act + (size_t)min(t + 1, t1 - 1) * j.S, sli, SLPR, j.S >> 5,
                                 nxt);
             XChunk xc[SCPL];
-            pair_xrow<SCPL>(scur, xc);
+            chunks_of_paired<SCPL>(scur, xc);
 #pragma unroll
             for (int c = 0; c < SCPL; ++c) scur[c] = nxt[c];
 #pragma unroll
@@ -749,7 +749,7 @@ __global__ __launch_bounds__(512) void decode_down_stream_kernel(DecodeJob j, in
         for (int b = 0; b < RB; ++b) load_wrow<CPL>(j.wd, e, d0 + b, lane, 64, cur[b]);
         const uint32_t sc = j.scores[p];
         XChunk xc[CPL];
-        pair_xrow<CPL>(xr, xc);
+        chunks_of_paired<CPL>(xr, xc);
         auto emit = [&](int r) __attribute__((always_inline)) {
 #pragma unroll
             for (int b = 0; b < RB; ++b) opaque_row(cur[b]);

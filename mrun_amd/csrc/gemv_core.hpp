@@ -153,4 +153,33 @@ __device__ __forceinline__ void pair_xrow(const XRaw *raw, XChunk *x) {
     for (int c = 0; c < CPL; ++c) pair_x(raw[c], x[c]);
 }
 
+// Rows that one GEMV writes for another to read (the decode's gate/up activations) are stored
+// already re-paired: element e of a row sits at paired_index(e), so that a chunk loads as the
+// XChunk words pair_x would build (dword 4w + i of a 32-element chunk holds elements 8w + i and
+// 8w + i + 4).
+__host__ __device__ constexpr int paired_index(int e) {
+    return (e & ~31) | (e & 24) | ((e & 3) << 1) | ((e >> 2) & 1);
+}
+
+// A chunk stored re-paired: the words as loaded, and their sum in pair_x's order (same bits).
+__device__ __forceinline__ void chunk_of_paired(const XRaw &r, XChunk &c) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        c.v[4 * w + 0] = r.a[w].x;
+        c.v[4 * w + 1] = r.a[w].y;
+        c.v[4 * w + 2] = r.a[w].z;
+        c.v[4 * w + 3] = r.a[w].w;
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s = dot2(c.v[i], 0x3F803F80u, s);
+    c.sum = s;
+}
+
+template <int CPL>
+__device__ __forceinline__ void chunks_of_paired(const XRaw *raw, XChunk *x) {
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) chunk_of_paired(raw[c], x[c]);
+}
+
 }  // namespace mrun
