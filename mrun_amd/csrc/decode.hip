@@ -341,13 +341,13 @@ __device__ __forceinline__ void qrouter_row(const bf16_t *x, int T, int D, const
 // K1: router logits + the shared expert's gate logit
 
 // QUANT: some rows are quantized (a separate instantiation, so the dense-router kernel keeps its
-// registers and schedule)
-template <int MAXT, bool NORM, bool QUANT>
-__global__ __launch_bounds__(256) void decode_router_kernel(DecodeJob j) {
+// registers and schedule). WPB waves (rows) per workgroup.
+template <int MAXT, bool NORM, bool QUANT, int WPB = 4>
+__global__ __launch_bounds__(64 * WPB) void decode_router_kernel(DecodeJob j) {
     // the wave index in a scalar register: the row, its weights and the branches below are the
     // wave's own (per-lane values would make every field of a quantized row a per-lane load)
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int r = blockIdx.x * 4 + wave;
+    const int r = blockIdx.x * WPB + wave;
     const int D = j.D;
     const bf16_t *w = nullptr, *bias = nullptr;
     bool quant = false;  // a quantized row instead (row qr of qw)
@@ -375,7 +375,7 @@ __global__ __launch_bounds__(256) void decode_router_kernel(DecodeJob j) {
         // workgroup 0 also writes them to j.x for K2. A row of D <= 2048 is read once.
         extern __shared__ __align__(16) bf16_t hs[];
         const uint4 ones = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
-        for (int t = wave; t < j.T; t += 4) {
+        for (int t = wave; t < j.T; t += WPB) {
             const bf16_t *src = j.norm_src + (size_t)t * D;
             bf16_t *hrow = &hs[(size_t)t * D], *grow = (bf16_t *)j.x + (size_t)t * D;
             if (D <= 2048) {
@@ -802,6 +802,16 @@ template <int MAXT>
 static void launch_k1(const DecodeJob &j, hipStream_t s) {
     dim3 grid((j.E + (j.S ? 1 : 0) + 3) / 4);
     const size_t lds = j.norm_src ? 2 * (size_t)j.T * j.D : 0;
+    if (j.T > 2 && !j.norm_src) {
+        // one row per workgroup from T = 3: every wave reads the T activation rows, so spreading
+        // the rows over all CUs spreads those reads (T = 16 66.75 -> 65.5 us per block, T = 8
+        // 40.8 -> 40.1, T = 4 26.35 -> 25.85; at T = 1 and 2, where the rows are one or two
+        // reads, four rows per workgroup stay faster: 14.1 -> 14.6 and 18.3 -> 18.6)
+        dim3 g1(j.E + (j.S ? 1 : 0));
+        if (!j.router || (j.S && !j.sh_gate_w)) decode_router_kernel<MAXT, false, true, 1><<<g1, 64, 0, s>>>(j);
+        else decode_router_kernel<MAXT, false, false, 1><<<g1, 64, 0, s>>>(j);
+        return;
+    }
     if (!j.router || (j.S && !j.sh_gate_w)) {  // a quantized router or shared gate
         if (j.norm_src) decode_router_kernel<MAXT, true, true><<<grid, 256, lds, s>>>(j);
         else decode_router_kernel<MAXT, false, true><<<grid, 256, 0, s>>>(j);
