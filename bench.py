@@ -585,7 +585,7 @@ def main(argv=None) -> int:
         return 0
     if args.gpus != 1:
         print("bench.py measures one GPU: the MoE block runs on a single MI355X in this build "
-              "(expert-parallel sharding is described in DESIGN.md, not implemented)",
+              "(expert-parallel sharding is designed but not implemented)",
               file=sys.stderr)
         return 2
 

@@ -7,8 +7,8 @@
 //! status whose message `mrun_last_error()` gives on the same thread (the facade's
 //! `Result<_, tensor::Error(String)>`, nuvec.rs:18-38). Tensors are caller-owned device memory;
 //! bf16 travels as `u16` bits. The safe layer (status to `tensor::Error`, `Array` to device
-//! pointers, the thread's stream and scratch) belongs to the engine: INTEGRATION.md in this
-//! repository shows it for `gather_qmm` and `SparseMoe::forward`.
+//! pointers, the thread's stream and scratch) belongs to the engine, around `gather_qmm` and
+//! `SparseMoe::forward`.
 //!
 //! This file is checked against the C headers by tests/test_rust_binding.py (names, argument
 //! order and types, struct layouts); this image has no Rust toolchain to compile it.
