@@ -341,13 +341,14 @@ __device__ __forceinline__ void qrouter_row(const bf16_t *x, int T, int D, const
 // K1: router logits + the shared expert's gate logit
 
 // QUANT: some rows are quantized (a separate instantiation, so the dense-router kernel keeps its
-// registers and schedule). WPB waves (rows) per workgroup.
-template <int MAXT, bool NORM, bool QUANT, int WPB = 4>
-__global__ __launch_bounds__(64 * WPB) void decode_router_kernel(DecodeJob j) {
+// registers and schedule). Four rows per workgroup, one per wave; TSPLIT (T > 2, no fused norm):
+// one row per workgroup, and wave w takes tokens [4w, 4w + 4) of it.
+template <int MAXT, bool NORM, bool QUANT, bool TSPLIT = false>
+__global__ __launch_bounds__(256) void decode_router_kernel(DecodeJob j) {
     // the wave index in a scalar register: the row, its weights and the branches below are the
     // wave's own (per-lane values would make every field of a quantized row a per-lane load)
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int r = blockIdx.x * WPB + wave;
+    const int r = TSPLIT ? (int)blockIdx.x : (int)blockIdx.x * 4 + wave;
     const int D = j.D;
     const bf16_t *w = nullptr, *bias = nullptr;
     bool quant = false;  // a quantized row instead (row qr of qw)
@@ -375,7 +376,7 @@ __global__ __launch_bounds__(64 * WPB) void decode_router_kernel(DecodeJob j) {
         // workgroup 0 also writes them to j.x for K2. A row of D <= 2048 is read once.
         extern __shared__ __align__(16) bf16_t hs[];
         const uint4 ones = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
-        for (int t = wave; t < j.T; t += WPB) {
+        for (int t = wave; t < j.T; t += 4) {
             const bf16_t *src = j.norm_src + (size_t)t * D;
             bf16_t *hrow = &hs[(size_t)t * D], *grow = (bf16_t *)j.x + (size_t)t * D;
             if (D <= 2048) {
@@ -411,6 +412,16 @@ __global__ __launch_bounds__(64 * WPB) void decode_router_kernel(DecodeJob j) {
         }
         __syncthreads();
         x = hs;
+    }
+    if (TSPLIT) {
+        const int tb = wave * 4;
+        if (tb >= j.T) return;
+        const int tn = min(4, j.T - tb);
+        x += (size_t)tb * D;
+        if (out) out += (size_t)tb * ldo;
+        if (w) router_row<4>(x, tn, D, w, first, bias, out, ldo, lane);
+        else if (QUANT && quant) qrouter_row<4>(x, tn, D, qw, qr, bias, out, ldo, lane);
+        return;
     }
     if (w) router_row<MAXT>(x, j.T, D, w, first, bias, out, ldo, lane);
     else if (QUANT && quant) qrouter_row<MAXT>(x, j.T, D, qw, qr, bias, out, ldo, lane);
@@ -803,13 +814,16 @@ static void launch_k1(const DecodeJob &j, hipStream_t s) {
     dim3 grid((j.E + (j.S ? 1 : 0) + 3) / 4);
     const size_t lds = j.norm_src ? 2 * (size_t)j.T * j.D : 0;
     if (j.T > 2 && !j.norm_src) {
-        // one row per workgroup from T = 3: every wave reads the T activation rows, so spreading
-        // the rows over all CUs spreads those reads (T = 16 66.75 -> 65.5 us per block, T = 8
-        // 40.8 -> 40.1, T = 4 26.35 -> 25.85; at T = 1 and 2, where the rows are one or two
-        // reads, four rows per workgroup stay faster: 14.1 -> 14.6 and 18.3 -> 18.6)
+        // one row per workgroup from T = 3, a wave per 4 tokens: every wave reads its tokens'
+        // activation rows, so spreading the rows over all CUs spreads those reads, and splitting
+        // the tokens over waves issues them at once (one row per single-wave workgroup: T = 16
+        // 66.75 -> 65.5 us per block, T = 8 40.8 -> 40.1, T = 4 26.35 -> 25.85; at T = 1 and 2,
+        // where the rows are one or two reads, four rows per workgroup stay faster: 14.1 -> 14.6
+        // and 18.3 -> 18.6)
         dim3 g1(j.E + (j.S ? 1 : 0));
-        if (!j.router || (j.S && !j.sh_gate_w)) decode_router_kernel<MAXT, false, true, 1><<<g1, 64, 0, s>>>(j);
-        else decode_router_kernel<MAXT, false, false, 1><<<g1, 64, 0, s>>>(j);
+        const int nt = 64 * ((j.T + 3) / 4);
+        if (!j.router || (j.S && !j.sh_gate_w)) decode_router_kernel<4, false, true, true><<<g1, nt, 0, s>>>(j);
+        else decode_router_kernel<4, false, false, true><<<g1, nt, 0, s>>>(j);
         return;
     }
     if (!j.router || (j.S && !j.sh_gate_w)) {  // a quantized router or shared gate
