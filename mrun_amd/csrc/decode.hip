@@ -11,7 +11,7 @@
 //                routing for K3.
 //   K3 down    : prefetches the shared expert's down rows, reads the routing, computes the routed
 //                down rows of every active expert for its 4 or 8 output rows and its group of
-//                tokens (two groups from T = 2), then the combine of those tokens:
+//                tokens (two groups from T = 2, four from T = 8), then the combine of those tokens:
 //                out = R(R(sum_j R(y[t,j] * s[t,j])) + R(R(sigmoid(g_t)) * shared[t])).
 // Rows wider than 2048 (the Coder shape): a K2 workgroup streams several row blocks pair by pair
 // with the next rows loaded before the current ones are computed, and without a shared expert K3
@@ -839,11 +839,14 @@ static void launch_k1(const DecodeJob &j, hipStream_t s) {
 template <int LPR, int CPL, int PB, int DR>
 static void launch_k3_pb(const DecodeJob &j, hipStream_t s);
 
-// K3 token groups: from T = 2 the tokens are split into two groups, each with its own workgroups
-// for every row block (twice the workgroups, half the pairs each, so each wave's chain of pair
-// batches is half as long). The split keeps every row's bits. T = 16 71.7 -> 66.7 us per block,
-// T = 4 28.3 -> 27.5, T = 2 18.8 -> 18.5; four groups at T = 16 measured 68.4.
-static int k3_token_groups(int T) { return T >= 2 ? 2 : 1; }
+// K3 token groups: from T = 2 the tokens are split into groups, each with its own workgroups for
+// every row block (more workgroups, fewer pairs each, so each wave's chain of pair batches is
+// shorter). The split keeps every row's bits. Two groups: T = 16 71.7 -> 66.7 us per block,
+// T = 4 28.3 -> 27.5, T = 2 18.8 -> 18.5. From T = 8 four groups with one pair per load batch
+// (fewer registers, so more waves per SIMD hide the batches' round trips): T = 16 63.15 -> 59.2,
+// T = 8 39.4 -> 38.8 (four groups with batches of 4 at T = 16: 68.4; eight groups: 60.4; one
+// pair per batch at T = 4: 25.55 -> 25.85).
+static int k3_token_groups(int T) { return T >= 8 ? 4 : (T >= 2 ? 2 : 1); }
 
 // K2 with RG rows per wave and NW waves per workgroup (I and S multiples of NW * RG). With rows
 // wider than 2048 (one row per wave), each workgroup streams gu_loop row blocks, the smallest
@@ -893,7 +896,8 @@ static void launch_k3_s(DecodeJob j, hipStream_t s) {
     constexpr int DR = 2 * (64 / LPR) > 4 ? 2 * (64 / LPR) : 4;
     constexpr int NRG = DR / (64 / LPR) > 0 ? DR / (64 / LPR) : 1;
     constexpr int PB = (NRG * CPL <= 2) ? 4 : (NRG * CPL <= 4 ? 2 : 1);
-    if (PB == 4 && (j.down_tokens * j.k + 3) / 4 <= 8) launch_k3_pb<LPR, CPL, 2, DR>(j, s);
+    if (j.T >= 8) launch_k3_pb<LPR, CPL, 1, DR>(j, s);
+    else if (PB == 4 && (j.down_tokens * j.k + 3) / 4 <= 8) launch_k3_pb<LPR, CPL, 2, DR>(j, s);
     else launch_k3_pb<LPR, CPL, PB, DR>(j, s);
 }
 
