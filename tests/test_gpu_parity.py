@@ -199,8 +199,9 @@ def test_swiglu_combine_norm():
 # ---------------------------------------------------------------------------------------------
 # the block
 
-# T = 3 and 5: the down launch's two token groups of unequal size
-@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 16])
+# T = 3, 5, 9 and 13: the down launch's token groups of unequal size (two groups below T = 8,
+# four from T = 8)
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 9, 13, 16])
 def test_block_decode_matches_oracle(q_host, q_dev, T):
     x_np = synth.make_x(Q, T, config=synth.CFG_DECODE, layer=T)
     run_block(q_host, q_dev, x_np, f"Q decode T={T}")
