@@ -32,7 +32,8 @@ constexpr int kMaxT = 16, kMaxP = 128;
 // Rows [row_base + g*RPI + rsub] of w0 (and w1 with glu), g < RG, for the pairs set in pm0|pm1
 // (bit p: pair p reads A row p / a_div and writes output row p). The next pair's activations are
 // loaded while the current pair is computed.
-template <int LPR, int CPL, int RG, bool GLU>
+// FULL: every row of the wave and every chunk of its lanes is in range (no masking).
+template <int LPR, int CPL, int RG, bool GLU, bool FULL = false>
 __device__ __forceinline__ void gemv_wave(const QW &w0, const QW &w1, int e, int row_base,
                                           const bf16_t *A, int lda, int a_div, uint64_t pm0,
                                           uint64_t pm1, bf16_t *out, int ldo, int lane) {
@@ -79,8 +80,8 @@ __device__ __forceinline__ void gemv_wave(const QW &w0, const QW &w1, int e, int
             float s0[RG], s1[RG];
 #pragma unroll
             for (int g = 0; g < RG; ++g) {
-                s0[g] = group_sum<64>(row_part(r0[g], xc));
-                s1[g] = group_sum<64>(row_part(r1[g], xc));
+                s0[g] = group_sum<64>(row_part<CPL, FULL>(r0[g], xc));
+                s1[g] = group_sum<64>(row_part<CPL, FULL>(r1[g], xc));
             }
             float a0 = s0[0], a1 = s1[0];
 #pragma unroll
@@ -97,8 +98,8 @@ __device__ __forceinline__ void gemv_wave(const QW &w0, const QW &w1, int e, int
 #pragma unroll
             for (int g = 0; g < RG; ++g) {
                 const int row = row_base + g * RPI + rsub;
-                const float a0 = group_sum<LPR>(row_part(r0[g], xc));
-                const float a1 = GLU ? group_sum<LPR>(row_part(r1[g], xc)) : 0.f;
+                const float a0 = group_sum<LPR>(row_part<CPL, FULL>(r0[g], xc));
+                const float a1 = GLU ? group_sum<LPR>(row_part<CPL, FULL>(r1[g], xc)) : 0.f;
                 if (li == 0 && row < w0.out) {
                     float v = a0;
                     if (GLU) {
@@ -504,7 +505,9 @@ __host__ __device__ inline int shared_gateup_blocks(const DecodeJob &j, int rows
 
 // (the streaming kernel with 3 chunks per lane is held to 168 registers, 3 waves per SIMD: at 171
 // it ran 2, and T = 1 took 4 us longer on the Coder shape)
-template <int LPR, int CPL, int RG, int NW, bool LOOP, bool SH_LAST>
+// FULL: D is exactly LPR * CPL chunks of 32 (rows are whole by construction: I and S are
+// multiples of the rows per workgroup).
+template <int LPR, int CPL, int RG, int NW, bool LOOP, bool SH_LAST, bool FULL = false>
 __global__ __launch_bounds__(64 * NW)
 __attribute__((amdgpu_waves_per_eu(LOOP && CPL == 3 ? 3 : 1))) void decode_gateup_kernel(
     DecodeJob j) {
@@ -598,8 +601,8 @@ __attribute__((amdgpu_waves_per_eu(LOOP && CPL == 3 ? 3 : 1))) void decode_gateu
                                    out + (size_t)p * ldo, lane);
         }
     } else {
-        gemv_wave<LPR, CPL, RG, true>(w0, w1, e, (rb * NW + wave) * RG * RPI, j.x, j.D, a_div, pm0,
-                                      pm1, out, ldo, lane);
+        gemv_wave<LPR, CPL, RG, true, FULL>(w0, w1, e, (rb * NW + wave) * RG * RPI, j.x, j.D,
+                                            a_div, pm0, pm1, out, ldo, lane);
     }
 }
 
@@ -864,7 +867,10 @@ static void launch_k2_l(const DecodeJob &j, int n_ch, dim3 g2, hipStream_t s) {
         if (j.T <= 2) go1(last);
         else go1(first);
     };
-    if (n_ch <= 64) go(decode_gateup_kernel<64, 1, RG, NW, LOOP, false>, decode_gateup_kernel<64, 1, RG, NW, LOOP, true>);
+    // whole rows of 2048 at T > 2 (4 rows per wave): the unmasked row math (T = 16 59.3 -> 58.15 us
+    // per block, T = 4 25.75 -> 25.55; at T <= 2 it measured no faster)
+    if (n_ch == 64 && !LOOP && RG == 4) go(decode_gateup_kernel<64, 1, RG, NW, false, false, true>, decode_gateup_kernel<64, 1, RG, NW, false, true, true>);
+    else if (n_ch <= 64) go(decode_gateup_kernel<64, 1, RG, NW, LOOP, false>, decode_gateup_kernel<64, 1, RG, NW, LOOP, true>);
     else if (n_ch <= 128) go(decode_gateup_kernel<64, 2, RG, NW, LOOP, false>, decode_gateup_kernel<64, 2, RG, NW, LOOP, true>);
     else if (n_ch <= 192) go(decode_gateup_kernel<64, 3, RG, NW, LOOP, false>, decode_gateup_kernel<64, 3, RG, NW, LOOP, true>);
     else go(decode_gateup_kernel<64, 4, RG, NW, LOOP, false>, decode_gateup_kernel<64, 4, RG, NW, LOOP, true>);

@@ -112,14 +112,15 @@ __device__ __forceinline__ void load_wrow(const QW &w, int e, int row, int li, i
     }
 }
 
-// Lane's part of row . x over its chunks: s * sum x (128 + q) + (b - 128 s) * sum x.
-template <int CPL>
+// Lane's part of row . x over its chunks: s * sum x (128 + q) + (b - 128 s) * sum x. FULL: the
+// caller's shape puts every chunk and row in range, so the `ok` masks are all set (same values).
+template <int CPL, bool FULL = false>
 __device__ __forceinline__ float row_part(const WRow<CPL> &r, const XChunk *x) {
     float a = 0.f;
     const bool has_b = (r.ok >> 31) & 1u;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
-        const bool ok = (r.ok >> c) & 1u;
+        const bool ok = FULL || ((r.ok >> c) & 1u);
         const float s = ok ? bf2f(r.s[c]) : 0.f;
         const float bp = ok ? (has_b ? bf2f(r.b[c]) : 0.f) - 128.f * s : 0.f;
         a += s * dot_chunk(r.q[c], x[c]) + bp * x[c].sum;
