@@ -867,9 +867,9 @@ static void launch_k2_l(const DecodeJob &j, int n_ch, dim3 g2, hipStream_t s) {
         if (j.T <= 2) go1(last);
         else go1(first);
     };
-    // whole rows of 2048 at T > 2 (4 rows per wave): the unmasked row math (T = 16 59.3 -> 58.15 us
-    // per block, T = 4 25.75 -> 25.55; at T <= 2 it measured no faster)
-    if (n_ch == 64 && !LOOP && RG == 4) go(decode_gateup_kernel<64, 1, RG, NW, false, false, true>, decode_gateup_kernel<64, 1, RG, NW, false, true, true>);
+    // whole rows of 2048 from T = 2: the unmasked row math (T = 16 59.3 -> 58.15 us per block,
+    // T = 4 25.75 -> 25.55, T = 2 18.15 -> 18.0; at T = 1 within the noise)
+    if (n_ch == 64 && !LOOP && (RG == 4 || j.T == 2)) go(decode_gateup_kernel<64, 1, RG, NW, false, false, true>, decode_gateup_kernel<64, 1, RG, NW, false, true, true>);
     else if (n_ch <= 64) go(decode_gateup_kernel<64, 1, RG, NW, LOOP, false>, decode_gateup_kernel<64, 1, RG, NW, LOOP, true>);
     else if (n_ch <= 128) go(decode_gateup_kernel<64, 2, RG, NW, LOOP, false>, decode_gateup_kernel<64, 2, RG, NW, LOOP, true>);
     else if (n_ch <= 192) go(decode_gateup_kernel<64, 3, RG, NW, LOOP, false>, decode_gateup_kernel<64, 3, RG, NW, LOOP, true>);

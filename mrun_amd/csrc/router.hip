@@ -196,7 +196,7 @@ __global__ __launch_bounds__(256) void topk_kernel(const bf16_t *__restrict__ lo
                                                    int k, int norm, bf16_t *__restrict__ gates,
                                                    uint32_t *__restrict__ ids,
                                                    bf16_t *__restrict__ scores) {
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int t = blockIdx.x * (int)(blockDim.x >> 6) + (int)(threadIdx.x >> 6);
     if (t >= T) return;
     topk_token(logits + (size_t)t * E, E, k, norm != 0, gates ? gates + (size_t)t * E : nullptr,
                ids + (size_t)t * k, scores + (size_t)t * k);
@@ -204,7 +204,9 @@ __global__ __launch_bounds__(256) void topk_kernel(const bf16_t *__restrict__ lo
 
 hipError_t launch_topk(const bf16_t *logits, int T, int E, int k, bool norm, bf16_t *gates,
                        uint32_t *ids, bf16_t *scores, hipStream_t stream) {
-    topk_kernel<<<(T + 3) / 4, 256, 0, stream>>>(logits, T, E, k, norm ? 1 : 0, gates, ids, scores);
+    // one token (one wave) per workgroup, so the tokens spread over CUs (T = 16 58.07 -> 57.87 us
+    // per block against four per workgroup)
+    topk_kernel<<<T, 64, 0, stream>>>(logits, T, E, k, norm ? 1 : 0, gates, ids, scores);
     return hipGetLastError();
 }
 
