@@ -146,3 +146,18 @@ def test_type_mapping_examples():
     assert c_type_to_rust("const mrun_bf16 **") == "*mut *const mrun_bf16"
     assert c_type_to_rust("void *") == "*mut c_void"
     assert c_type_to_rust("void") == "()"
+
+
+def test_manifest_with_links_has_a_build_script():
+    """Cargo rejects a manifest that declares `links` without a build script; the script must name
+    the library the `links` key declares."""
+    manifest = (ROOT / "bindings" / "rust" / "Cargo.toml").read_text()
+    m = re.search(r'^links\s*=\s*"([^"]+)"', manifest, flags=re.M)
+    if m is None:
+        return
+    script = ROOT / "bindings" / "rust" / re.search(r'^build\s*=\s*"([^"]+)"', manifest, flags=re.M).group(1) \
+        if re.search(r'^build\s*=', manifest, flags=re.M) else ROOT / "bindings" / "rust" / "build.rs"
+    assert script.exists(), "links without a build script"
+    text = script.read_text()
+    assert f"cargo:rustc-link-lib=dylib={m.group(1)}" in text
+    assert "fn main()" in text
