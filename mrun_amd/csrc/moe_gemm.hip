@@ -165,6 +165,15 @@ __device__ __forceinline__ const T *unip(const T *p) {
 __device__ __forceinline__ int swz_a(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 __device__ __forceinline__ int swz_c(int r) { return ((r >> 2) ^ (r >> 1)) & 3; }
 
+// The tile row whose act column sum lane `l` holds after the gate/up epilogue's reduce-scatter:
+// with fr = l % 32, bit 4 of fr chose the row fragment (32 rows), bits 3-2 the 8-row block,
+// bits 1-0 the row in a block of 4, and the lane half (l / 32) the block of 4 within 8 (the
+// MFMA's C layout: value i of lane l is row 8 (i / 4) + 4 (l / 32) + i % 4 of its fragment).
+__device__ __forceinline__ int xrow_of(int l) {
+    const int fr = l & 31;
+    return 32 * (fr >> 4) + 8 * ((fr >> 2) & 3) + 4 * (l >> 5) + (fr & 3);
+}
+
 template <bool GLU>
 __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
     using namespace mg;
@@ -563,9 +572,12 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
         sc_pend = 0.f;
 
         // ---- epilogue of item ci. Stores are widened by exchanging values between lanes (DPP):
-        // a 2-byte store per lane and value costs about as much as a 16-byte one.
+        // a 2-byte store per lane and value costs about as much as a 16-byte one. They go through
+        // a buffer resource over the tile's own rows (from row0, mrows rows), so that the stores
+        // of the rows past mrows fall outside it and are dropped: no branch per store.
         bf16_t *out = ci.sh ? j.sh.out : j.out;
         const int ldo = ci.sh ? j.sh.ldo : j.ldo;
+        const rsrc_t r_out = rsrc_of(out + (size_t)ci.row0 * ldo, (uint32_t)ci.mrows * (uint32_t)ldo * 2u);
         if (GLU) {
             // act = R(silu(R(gate)) * R(up)), stored packed; and this wave's half of the act rows'
             // group sums (the down product's X)
@@ -576,51 +588,73 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
             // the pair of row i + 1: both at the packed position of jj & 3
             const int pcol = (col & ~63) + 8 * (2 * (kb & 3) + (kb >> 2)) + 2 * (jj & 3);
             const bool hi4 = (jj & 4) != 0;
-            float xsum = 0.f;  // the half-group sum of tile row `lane`
+            float va[2][16];  // the act values (rounded) of rows mi * 32 + 8 (i / 4) + 4 fh + i % 4
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
                 for (int i = 0; i < 16; i += 2) {
-                    uint32_t h[2];
-                    float sum2[2];
+                    float v[2];
 #pragma unroll
                     for (int d = 0; d < 2; ++d) {
-                        const float g = rbf(acc[mi][0][i + d]), u = rbf(acc[mi][1][i + d]);
+                        const uint32_t gu = f2bf2(acc[mi][0][i + d], acc[mi][1][i + d]);
+                        const float g = bf_lo(gu), u = bf_hi(gu);
                         // silu(g) = g / (1 + exp(-g)): v_exp and v_rcp (within 2 f32 ulp)
                         const float e = __builtin_amdgcn_exp2f(-1.44269504088896f * g);
-                        const float v = rbf((g * __builtin_amdgcn_rcpf(1.f + e)) * u);
-                        h[d] = __float_as_uint(v) >> 16;
-                        // sum over the 32 columns of this lane half: rows of 16 lanes, row pairs
-                        float sm = row_sum16(v);
-                        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x142,
-                                                                         0xA, 0xF, false));
-                        sum2[d] = sm;
+                        v[d] = (g * __builtin_amdgcn_rcpf(1.f + e)) * u;
                     }
+                    const uint32_t hv = f2bf2(v[0], v[1]);  // row i in the low half, i + 1 high
+                    va[mi][i] = bf_lo(hv), va[mi][i + 1] = bf_hi(hv);
                     // lane l (jj < 4) keeps row i of (jj, jj + 4); lane l + 4 row i + 1
-                    const uint32_t send = hi4 ? h[0] : h[1];
+                    const uint32_t send = hi4 ? (hv & 0xFFFFu) : (hv >> 16);
                     const uint32_t from_up = (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0x104, 0xF, 0xF, false);   // lane l + 4
                     const uint32_t from_dn = (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0x114, 0xF, 0xF, false);   // lane l - 4
-                    const uint32_t pair = hi4 ? (from_dn | (h[1] << 16)) : (h[0] | (from_up << 16));
+                    const uint32_t pair = hi4 ? (from_dn | (hv & 0xFFFF0000u)) : ((hv & 0xFFFFu) | (from_up << 16));
                     const int r = mi * 32 + 8 * (i >> 2) + 4 * fh + (i & 3) + (hi4 ? 1 : 0);
-                    if (r < ci.mrows)
-                        *(uint32_t *)(out + (size_t)(ci.row0 + r) * ldo + pcol) = pair;
-                    // row sums: lanes 16-31 hold the lane-half-0 rows, 48-63 the lane-half-1 rows
-#pragma unroll
-                    for (int d = 0; d < 2; ++d) {
-                        const int r0 = mi * 32 + 8 * ((i + d) >> 2) + ((i + d) & 3);
-                        const int s0 = __builtin_amdgcn_readlane(__float_as_int(sum2[d]), 16);
-                        const int s1 = __builtin_amdgcn_readlane(__float_as_int(sum2[d]), 48);
-                        int xs = __float_as_int(xsum);
-                        asm("v_writelane_b32 %0, %1, %2" : "+v"(xs) : "s"(s0), "i"(r0));
-                        asm("v_writelane_b32 %0, %1, %2" : "+v"(xs) : "s"(s1), "i"(r0 + 4));
-                        xsum = __int_as_float(xs);
-                    }
+                    __builtin_amdgcn_raw_buffer_store_b32(pair, r_out, (r * ldo + pcol) * 2, 0, 0);
                 }
+            // this wave's sums of the 32 act columns for each row, by a reduce-scatter over the
+            // 32 lanes of each lane half (their columns): every step pairs lane l with lane l ^ d,
+            // each keeps the half of its values that its bit d selects and adds the partner's
+            // copy of it. After d = 16 (permlane16_swap), 8 (row_ror:8), 4 (row_shl/shr:4 by
+            // banks), 2 and 1 (quad_perm) the lane holds the sum of row xrow_of(lane).
+            float w16[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {  // d = 16: lanes of even rows keep mi = 0, odd rows 1
+                const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(va[0][i]),
+                                                                __float_as_uint(va[1][i]), false, false);
+                w16[i] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+            }
+            const bool b3 = (lane & 8) != 0, b2 = (lane & 4) != 0, b1 = (lane & 2) != 0, b0 = (lane & 1) != 0;
+            float w8[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {  // d = 8: keep i + 8 b3
+                const float keep = b3 ? w16[i + 8] : w16[i], send = b3 ? w16[i] : w16[i + 8];
+                w8[i] = keep + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), 0x128, 0xF, 0xF, false));
+            }
+            float w4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {  // d = 4: keep i + 4 b2
+                const float keep = b2 ? w8[i + 4] : w8[i], send = b2 ? w8[i] : w8[i + 4];
+                int m = __builtin_amdgcn_update_dpp(0, __float_as_int(send), 0x104, 0xF, 0x5, false);  // banks 0, 2: lane l + 4
+                m = __builtin_amdgcn_update_dpp(m, __float_as_int(send), 0x114, 0xF, 0xA, false);      // banks 1, 3: lane l - 4
+                w4[i] = keep + __int_as_float(m);
+            }
+            float w2[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {  // d = 2: keep i + 2 b1
+                const float keep = b1 ? w4[i + 2] : w4[i], send = b1 ? w4[i] : w4[i + 2];
+                w2[i] = keep + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), 0x4E, 0xF, 0xF, false));
+            }
+            {  // d = 1: keep b0
+                const float keep = b0 ? w2[1] : w2[0], send = b0 ? w2[0] : w2[1];
+                x_pend = keep + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), 0xB1, 0xF, 0xF, false));
+            }
             // the group sum is this wave's half plus its partner's (waves 2h, 2h + 1 cover group
-            // n0 / 64 + h); the hand-over runs after the next barriers
-            x_pend = xsum;
-            x_dst = lane < ci.mrows
-                        ? OX + (size_t)(ci.row0 + lane) * 3 * x_oxe + (ci.n0 >> 6) + (wave >> 1)
+            // n0 / 64 + h, with the same lane-to-row map); the hand-over runs after the next
+            // barriers
+            const int xr = xrow_of(lane);
+            x_dst = xr < ci.mrows
+                        ? OX + (size_t)(ci.row0 + xr) * 3 * x_oxe + (ci.n0 >> 6) + (wave >> 1)
                         : nullptr;
             x_state = 1;
         } else {
@@ -634,9 +668,8 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
                 for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
                     for (int b = 0; b < 4; ++b) {
-                        const uint32_t h0 = f2bf(acc[mi][ni][4 * b]), h1 = f2bf(acc[mi][ni][4 * b + 1]);
-                        const uint32_t h2 = f2bf(acc[mi][ni][4 * b + 2]), h3 = f2bf(acc[mi][ni][4 * b + 3]);
-                        const uint32_t p02 = h0 | (h2 << 16), p13 = h1 | (h3 << 16);
+                        const uint32_t p02 = f2bf2(acc[mi][ni][4 * b], acc[mi][ni][4 * b + 2]);
+                        const uint32_t p13 = f2bf2(acc[mi][ni][4 * b + 1], acc[mi][ni][4 * b + 3]);
                         // lanes q, q ^ 1: even lanes gather rows 0 and 2, odd lanes rows 1 and 3
                         const uint32_t own = (q & 1) ? p13 : p02;
                         const uint32_t rcv = (uint32_t)__builtin_amdgcn_mov_dpp((int)((q & 1) ? p02 : p13), 0xB1, 0xF, 0xF, false);
@@ -647,7 +680,8 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
                         const uint32_t r2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)((q & 2) ? A : B), 0x4E, 0xF, 0xF, false);
                         const uint2 w = (q & 2) ? make_uint2(r2, B) : make_uint2(A, r2);
                         const int r = mi * 32 + 8 * b + 4 * fh + q;
-                        if (r < ci.mrows) *(uint2 *)(out + (size_t)(ci.row0 + r) * ldo + col4) = w;
+                        typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+                        __builtin_amdgcn_raw_buffer_store_b64(u32x2{w.x, w.y}, r_out, (r * ldo + col4) * 2, 0, 0);
                     }
             }
         }
