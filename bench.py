@@ -429,6 +429,82 @@ def prefill_point(args, Q, M, synth, torch) -> dict:
             / (stages["down"] * 1e-6) / MFMA_BF16_PEAK}
 
 
+def time_call(fn, reps: int, torch, warmup: int = 5) -> float:
+    """Mean device ms of fn() over reps calls, HIP events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def facade_point(args, Q, M, synth, torch) -> dict:
+    """The facade ops at configs[2]'s prefill size: gather_qmm over the T k = 16,384 pair rows of
+    the gate projection in SwitchGlu's sorted case (moe.rs:62-80: rows gathered by token, indices
+    ascending, one row per index), and quantized_matmul over T = 2048 rows of the shared expert's
+    gate projection. Each call's permute, packing and reordering are inside the timed region."""
+    print("[bench] facade gather_qmm / quantized_matmul at configs[2] sizes", file=sys.stderr,
+          flush=True)
+    hz = synth.make_block(Q, config=synth.CFG_PREFILL_ZIPF, zipf=True)
+    dz = M.SparseMoe(hz)
+    T, k, D, I, S = 2048, Q.top_k, Q.hidden, Q.intermediate, Q.shared
+    xz = M.bf16_tensor(synth.make_x(Q, T, config=synth.CFG_PREFILL_ZIPF))
+    _, _, ids, _ = dz.router_forward(xz)
+    flat = ids.reshape(-1).to(torch.int64)
+    order = torch.sort(flat, stable=True).indices
+    idx = flat[order].to(torch.int32).contiguous()
+    rows = xz[order // k].contiguous()
+    n = idx.numel()
+    reps = max(args.steps // 8, 10)
+    ms_g = time_call(lambda: M.gather_qmm(rows, dz.gate_proj, idx, sorted_indices=True), reps, torch)
+    fl_g = 2.0 * n * I * D
+    xs = xz.contiguous()
+    ms_q = time_call(lambda: M.quantized_matmul(xs, dz.sh_gate_proj), reps, torch)
+    fl_q = 2.0 * T * S * D
+    return {"gather_qmm": {"rows": n, "out": I, "in": D, "device_ms": ms_g, "flops": fl_g,
+                           "mfma_frac": fl_g / (ms_g * 1e-3) / MFMA_BF16_PEAK,
+                           "kernel": "moe_gemm_kernel (packed x, permute and row reorder included)"},
+            "quantized_matmul": {"rows": T, "out": S, "in": D, "device_ms": ms_q, "flops": fl_q,
+                                 "mfma_frac": fl_q / (ms_q * 1e-3) / MFMA_BF16_PEAK,
+                                 "kernel": "qgemm_kernel (no workspace in the facade signature)"}}
+
+
+def formats_point(args, Q, M, synth, torch) -> dict:
+    """The other expert formats the reference loads (load.rs:15-17) on the configs[1]/[2] block:
+    8-bit experts (group 64) and 4-bit experts with group 32, decode T = 1 and 16 and prefill
+    T = 2048 (Zipf router)."""
+    out = {}
+    for name, shape, bits in (("experts8_g64", Q, 8),
+                              ("experts4_g32", synth.Shape(hidden=Q.hidden, experts=Q.experts,
+                                                           top_k=Q.top_k, intermediate=Q.intermediate,
+                                                           shared=Q.shared, group=32), 4)):
+        print(f"[bench] formats: {name}", file=sys.stderr, flush=True)
+        pt = {}
+        hb = synth.make_block(shape, config=synth.CFG_DECODE, expert_bits=bits)
+        dv = M.SparseMoe(hb)
+        for T in (1, 16):
+            x = M.bf16_tensor(synth.make_x(shape, T, config=synth.CFG_DECODE, layer=T))
+            wall, dev_ms, _ = time_forward(dv, x, max(args.steps // 4, 20), args.warmup, torch)
+            pt[f"decode_T{T}"] = {"device_ms": dev_ms, "ms_per_step": wall,
+                                  "tokens_per_s": T / (wall * 1e-3)}
+        del dv, hb
+        hz = synth.make_block(shape, config=synth.CFG_PREFILL_ZIPF, zipf=True, expert_bits=bits)
+        dz = M.SparseMoe(hz)
+        xz = M.bf16_tensor(synth.make_x(shape, 2048, config=synth.CFG_PREFILL_ZIPF))
+        wall, dev_ms, _ = time_forward(dz, xz, max(args.steps // 8, 10), 10, torch)
+        fl = prefill_flops(shape, 2048)
+        pt["prefill_T2048"] = {"device_ms": dev_ms, "tokens_per_s": 2048 / (wall * 1e-3),
+                               "block_mfma_frac": fl["block"] / (dev_ms * 1e-3) / MFMA_BF16_PEAK}
+        del dz, hz
+        out[name] = pt
+    return out
+
+
 def stack_point(args, Q, M, synth, torch) -> dict:
     """40 MoE layers with their own seeded weights (generated on the device: about
     18 GB), pre-RMSNorm (eps 1e-6, weight 1) and the residual add, at T = 1 decode and T = 4096
@@ -571,6 +647,8 @@ def main(argv=None) -> int:
                     help="only the configs[3] layer stack; prints its own JSON line")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the configs[2] prefill point (for profilers); prints its own JSON line")
+    ap.add_argument("--facade-only", action="store_true",
+                    help="only the facade-op and expert-format points; prints its own JSON line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device to device 10 times (the byte counters' reference)")
     args = ap.parse_args(argv)
@@ -602,6 +680,10 @@ def main(argv=None) -> int:
         return 0
     if args.coder_only:
         print(json.dumps({"coder": coder_point(args, M, synth, torch)}), flush=True)
+        return 0
+    if args.facade_only:
+        print(json.dumps({"facade": facade_point(args, Q, M, synth, torch),
+                          "formats": formats_point(args, Q, M, synth, torch)}), flush=True)
         return 0
     print(f"[bench] generating the configs[1] block ({Q.name})", file=sys.stderr, flush=True)
     hb = synth.make_block(Q, config=synth.CFG_DECODE)
@@ -680,6 +762,8 @@ def main(argv=None) -> int:
         del d8, h8
 
     prefill = None if args.no_prefill else prefill_point(args, Q, M, synth, torch)
+    facade = None if args.no_prefill else facade_point(args, Q, M, synth, torch)
+    formats = None if args.no_sweep else formats_point(args, Q, M, synth, torch)
     stack = None if args.no_stack else stack_point(args, Q, M, synth, torch)
     coder = None if args.no_coder else coder_point(args, M, synth, torch, cold)
 
@@ -725,6 +809,8 @@ def main(argv=None) -> int:
         "sweep": sweep,
         "gates8": gates8,
         "prefill": prefill,
+        "facade": facade,
+        "formats": formats,
         "stack": stack,
         "coder": coder,
     }

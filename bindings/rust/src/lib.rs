@@ -197,7 +197,8 @@ extern "C" {
         workspace_bytes: usize,
         stream: mrun_stream_t,
     ) -> c_int;
-    pub fn mrun_gather_qmm_workspace_bytes(n: i32, experts: i32) -> usize;
+    pub fn mrun_gather_qmm_workspace_bytes(n: i32, experts: i32, x_rows: i32, in_: i32, out: i32)
+        -> usize;
     /// `tensor::quantized_matmul` (nuvec.rs:660-663).
     pub fn mrun_quantized_matmul(
         x: *const mrun_bf16,

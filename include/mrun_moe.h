@@ -177,7 +177,11 @@ size_t mrun_moe_permute_workspace_bytes(int32_t pairs, int32_t experts);
 int mrun_gather_qmm(const mrun_bf16 *x, int32_t x_rows, const mrun_quantized *w,
                     const uint32_t *indices, int32_t n, int32_t sorted_indices, mrun_bf16 *out,
                     void *workspace, size_t workspace_bytes, mrun_stream_t stream);
-size_t mrun_gather_qmm_workspace_bytes(int32_t n, int32_t experts);
+/* Workspace of mrun_gather_qmm for n indices over `experts` experts, x [x_rows, in], out width
+ * `out` (the routing of the indices and, above 16 indices, the grouped GEMM's packed x and its
+ * output in expert order). */
+size_t mrun_gather_qmm_workspace_bytes(int32_t n, int32_t experts, int32_t x_rows, int32_t in,
+                                       int32_t out);
 
 /* tensor::quantized_matmul (nuvec.rs:660-663): out [rows, w->out] = x . dequant(w)^T, w with
  * experts = 1. */

@@ -109,7 +109,7 @@ SIGNATURES = {
         [c_void_p, c_int32, POINTER(Quantized), c_void_p, c_int32, c_int32, c_void_p, c_void_p,
          c_size_t, c_void_p],
     ),
-    "mrun_gather_qmm_workspace_bytes": (c_size_t, [c_int32, c_int32]),
+    "mrun_gather_qmm_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32, c_int32, c_int32]),
     "mrun_quantized_matmul": (c_int32, [c_void_p, c_int32, POINTER(Quantized), c_void_p, c_void_p]),
     "mrun_linear_forward": (c_int32, [POINTER(Linear), c_void_p, c_int32, c_void_p, c_void_p]),
     "mrun_swiglu": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),

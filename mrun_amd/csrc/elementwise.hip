@@ -276,6 +276,28 @@ hipError_t launch_fill_u32(uint32_t *dst, uint32_t v, int n, hipStream_t stream)
     return hipGetLastError();
 }
 
+// dst[r] = src[map[r]] for rows of `width` bf16 (a multiple of 8), 16 bytes per thread.
+__global__ __launch_bounds__(256) void rows_gather_kernel(const bf16_t *__restrict__ src,
+                                                          const uint32_t *__restrict__ map,
+                                                          int rows, int width,
+                                                          bf16_t *__restrict__ dst) {
+    const int chunks = width / 8;
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long long)rows * chunks) return;
+    const int r = (int)(i / chunks), c = (int)(i % chunks);
+    *(uint4 *)(dst + (size_t)r * width + (size_t)c * 8) =
+        *(const uint4 *)(src + (size_t)map[r] * width + (size_t)c * 8);
+}
+
+hipError_t launch_rows_gather(const bf16_t *src, const uint32_t *map, int rows, int width,
+                              bf16_t *dst, hipStream_t stream) {
+    const long long n = (long long)rows * (width / 8);
+    if (n <= 0) return hipSuccess;
+    if (width % 8 != 0) return hipErrorInvalidValue;
+    rows_gather_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(src, map, rows, width, dst);
+    return hipGetLastError();
+}
+
 // y[t][n] = R(x[t] . W[n]) (then R(. + bias[n])) for narrow outputs (a Linear with few rows, e.g.
 // the shared expert's gate): one wave per token, the rows of W in turn.
 __global__ __launch_bounds__(256) void rowdot_kernel(const bf16_t *__restrict__ x, int T, int D,

@@ -201,6 +201,7 @@ constexpr int kGemmTileN = 64;
 struct MoeGemmJob {
     const bf16_t *A;
     int lda;
+    int a_rows;  // rows of A (its byte offsets are 32-bit: a_rows * lda * 2 < 2^32)
     const bf16_t *AX;
     int ax_e;
     const uint32_t *tile_rows;
@@ -278,5 +279,8 @@ hipError_t launch_rowdot(const bf16_t *x, int T, int D, const bf16_t *W, int N,
 hipError_t launch_add_bias(bf16_t *y, const bf16_t *bias, int rows, int n, hipStream_t stream);
 // dst[0..n) = v (a kernel, not a memset node, so that captured graphs replay it faithfully)
 hipError_t launch_fill_u32(uint32_t *dst, uint32_t v, int n, hipStream_t stream);
+// dst[r] = src[map[r]], r < rows, rows of `width` bf16 (width % 8 == 0; 16-byte aligned rows)
+hipError_t launch_rows_gather(const bf16_t *src, const uint32_t *map, int rows, int width,
+                              bf16_t *dst, hipStream_t stream);
 
 }  // namespace mrun

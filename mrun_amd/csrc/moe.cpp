@@ -466,13 +466,13 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
     MoeGemmJob mg{}, md{};
     bool new_path = false, fuse_new = false;
     if (mfma && T > 16) {
-        mg.A = (const bf16_t *)at(p.xp), mg.lda = D, mg.AX = (const bf16_t *)at(p.xs);
+        mg.A = (const bf16_t *)at(p.xp), mg.lda = D, mg.a_rows = T, mg.AX = (const bf16_t *)at(p.xs);
         mg.ax_e = D / 64, mg.tile_rows = (const uint32_t *)at(p.tile_rows);
         mg.K = D, mg.N = I, mg.glu = 1;
         mg.w0 = qw_of(m.switch_gate_proj), mg.w1 = qw_of(m.switch_up_proj);
         mg.routing = rt, mg.has_routing = 1, mg.max_tiles = p.max_tiles;
         mg.out = act, mg.ldo = I, mg.OX = (bf16_t *)at(p.act_x);
-        md.A = act, md.lda = I, md.AX = (const bf16_t *)at(p.act_x), md.ax_e = I / 64;
+        md.A = act, md.lda = I, md.a_rows = P, md.AX = (const bf16_t *)at(p.act_x), md.ax_e = I / 64;
         md.K = I, md.N = D, md.glu = 0, md.w0 = qw_of(m.switch_down_proj);
         md.routing = rt, md.has_routing = 1, md.max_tiles = p.max_tiles, md.out = y, md.ldo = D;
         new_path = moe_gemm_supported(mg) && moe_gemm_supported(md);
@@ -509,7 +509,7 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
             st.mark(s);
             st.mark(s);
         }
-    } else if (mfma) {
+    } else if (mfma && T > 16) {  // at decode sizes the gathered GEMV streams the rows once
         GemmJob g{};
         g.A = x, g.lda = D, g.a_map = po.order, g.a_div = k, g.N = I, g.K = D;
         g.w0 = qw_of(m.switch_gate_proj), g.w1 = qw_of(m.switch_up_proj);
@@ -804,11 +804,45 @@ int mrun_moe_workspace_routing(const mrun_moe_config *cfg, int32_t tokens, size_
     return report(st);
 }
 
-size_t mrun_gather_qmm_workspace_bytes(int32_t n, int32_t experts) {
-    if (n <= 0 || experts <= 0 || experts > 1024) return 0;
-    const size_t max_tiles = (size_t)(n + kGemmTileM - 1) / kGemmTileM + experts;
-    return a256(4 * ((size_t)experts + 1)) + a256(4 * (size_t)n) + a256(4 * (size_t)experts) +
-           a256(4) + a256(12 * max_tiles) + a256(4) + a256(4 * permute_counts_words(n, experts));
+// gather_qmm's workspace: the routing of its indices and, above 16 indices, the grouped GEMM's
+// operands (x packed with its group sums, each tile's x rows) and its output in expert order.
+struct GqPlan {
+    size_t offsets, order, inverse, active, n_active, tiles, n_tiles, counts, xp, xs, tile_rows, ys;
+    size_t total;
+    size_t max_tiles;
+};
+
+static GqPlan gq_plan(int n, int experts, int x_rows, int in, int out) {
+    GqPlan p{};
+    size_t at = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = at;
+        at += a256(bytes);
+        return o;
+    };
+    p.max_tiles = (size_t)(n + kGemmTileM - 1) / kGemmTileM + experts;
+    p.offsets = take(4 * ((size_t)experts + 1));
+    p.order = take(4 * (size_t)n);
+    p.active = take(4 * (size_t)experts);
+    p.n_active = take(4);
+    p.tiles = take(12 * p.max_tiles);
+    p.n_tiles = take(4);
+    p.counts = take(4 * permute_counts_words(n, experts));
+    if (n > 16) {
+        p.inverse = take(4 * (size_t)n);
+        p.xp = take(2 * (size_t)x_rows * in);
+        p.xs = take(2 * 3 * (size_t)x_rows * (in / 64));
+        p.tile_rows = take(4 * p.max_tiles * kGemmTileM);
+        p.ys = take(2 * (size_t)n * out);
+    }
+    p.total = at;
+    return p;
+}
+
+size_t mrun_gather_qmm_workspace_bytes(int32_t n, int32_t experts, int32_t x_rows, int32_t in,
+                                       int32_t out) {
+    if (n <= 0 || experts <= 0 || experts > 1024 || x_rows <= 0 || in <= 0 || out <= 0) return 0;
+    return gq_plan(n, experts, x_rows, in, out).total;
 }
 
 int mrun_gather_qmm(const mrun_bf16 *x, int32_t x_rows, const mrun_quantized *w,
@@ -826,31 +860,48 @@ int mrun_gather_qmm(const mrun_bf16 *x, int32_t x_rows, const mrun_quantized *w,
     if (st.ok()) st = check_ptr(x, "x");
     if (st.ok()) st = check_ptr(out, "out");
     if (st.ok() && w->experts > 1024) st = Err(MRUN_ERR_UNSUPPORTED, "more than 1024 experts");
-    const size_t need = mrun_gather_qmm_workspace_bytes(n, w ? w->experts : 1);
+    const size_t need =
+        st.ok() ? mrun_gather_qmm_workspace_bytes(n, w->experts, x_rows, w->in, w->out) : 0;
     if (st.ok() && (!workspace || workspace_bytes < need))
         st = Err(MRUN_ERR_WORKSPACE, "gather_qmm needs " + std::to_string(need) + " bytes");
     if (st.ok()) {
         hipStream_t s = (hipStream_t)stream;
         char *ws = (char *)workspace;
-        const int E = w->experts;
-        const size_t max_tiles = (size_t)(n + kGemmTileM - 1) / kGemmTileM + E;
+        const int E = w->experts, per_x = n / x_rows;
+        const GqPlan p = gq_plan(n, E, x_rows, w->in, w->out);
+        auto u32 = [&](size_t off) { return (uint32_t *)(ws + off); };
         PermuteOut po{};
-        size_t at = 0;
-        po.offsets = (uint32_t *)(ws + at), at += a256(4 * ((size_t)E + 1));
-        po.order = (uint32_t *)(ws + at), at += a256(4 * (size_t)n);
-        po.active = (uint32_t *)(ws + at), at += a256(4 * (size_t)E);
-        po.n_active = (uint32_t *)(ws + at), at += a256(4);
-        po.tiles = (uint32_t *)(ws + at), at += a256(12 * max_tiles);
-        po.n_tiles = (uint32_t *)(ws + at), at += a256(4);
+        po.offsets = u32(p.offsets), po.order = u32(p.order), po.active = u32(p.active);
+        po.n_active = u32(p.n_active), po.tiles = u32(p.tiles), po.n_tiles = u32(p.n_tiles);
         po.tile_m = kGemmTileM;
-        uint32_t *counts = (uint32_t *)(ws + at);
-        st = hip_status(launch_permute(indices, n, 1, E, counts, po, s), "gather_qmm permute");
         Routing rt{po.offsets, po.active, po.n_active, po.tiles, po.n_tiles};
-        const int per_x = n / x_rows;
-        if (st.ok() && n > 16 && w->in % 64 == 0) {
+        // the tuned grouped GEMM (4-bit group 64, in % 512, out % 256): x packed, the tiles' x
+        // rows from the permute, the product in expert order, then each index's row in place
+        MoeGemmJob mj{};
+        if (n > 16) {
+            mj.A = (const bf16_t *)(ws + p.xp), mj.lda = w->in, mj.a_rows = x_rows;
+            mj.AX = (const bf16_t *)(ws + p.xs);
+            mj.ax_e = w->in / 64, mj.tile_rows = u32(p.tile_rows), mj.K = w->in, mj.N = w->out;
+            mj.glu = 0, mj.w0 = qw_of(*w), mj.routing = rt, mj.has_routing = 1;
+            mj.max_tiles = (int)p.max_tiles, mj.out = (bf16_t *)(ws + p.ys), mj.ldo = w->out;
+        }
+        const bool tuned = n > 16 && moe_gemm_supported(mj);
+        if (tuned) po.inverse = u32(p.inverse), po.tile_rows = u32(p.tile_rows);
+        st = hip_status(launch_permute(indices, n, tuned ? per_x : 1, E, u32(p.counts), po, s),
+                        "gather_qmm permute");
+        if (st.ok() && tuned) {
+            st = hip_status(launch_apack(x, w->in, x_rows, w->in, (bf16_t *)(ws + p.xp), w->in,
+                                         (bf16_t *)(ws + p.xs), s),
+                            "gather_qmm pack x");
+            if (st.ok()) st = hip_status(launch_moe_gemm(mj, s), "gather_qmm (moe gemm)");
+            if (st.ok())
+                st = hip_status(launch_rows_gather((const bf16_t *)(ws + p.ys), po.inverse, n, w->out,
+                                                   out, s),
+                                "gather_qmm rows");
+        } else if (st.ok() && n > 16 && w->in % 64 == 0) {
             GemmJob j{};
             j.A = x, j.lda = w->in, j.a_map = po.order, j.a_div = per_x, j.N = w->out, j.K = w->in;
-            j.w0 = qw_of(*w), j.routing = rt, j.has_routing = 1, j.max_tiles = (int)max_tiles;
+            j.w0 = qw_of(*w), j.routing = rt, j.has_routing = 1, j.max_tiles = (int)p.max_tiles;
             j.o_map = po.order, j.out = out, j.ldo = w->out;
             st = hip_status(launch_gemm(j, s), "gather_qmm (mfma)");
         } else if (st.ok()) {

@@ -723,6 +723,9 @@ bool moe_gemm_supported(const MoeGemmJob &j) {
     };
     const int ncols = j.glu ? 128 : 256;
     if (j.N <= 0 || j.N % ncols != 0 || !ok(j.w0, j.K) || (j.glu && !ok(j.w1, j.K))) return false;
+    // A row offsets (row * lda * 2 bytes, through a buffer resource) are 32-bit
+    auto a_fits = [](long long rows, int lda) { return rows > 0 && rows * lda * 2 < (1LL << 32); };
+    if (!a_fits(j.a_rows, j.lda) || (j.has_shared && !a_fits(j.sh.M, j.sh.lda))) return false;
     if (j.w0.out != j.N || (j.glu && j.w1.out != j.N)) return false;
     // X splits: one entry per group of x (gate/up) or of act (down)
     const int axe = j.K / 64;

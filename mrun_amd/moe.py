@@ -344,7 +344,7 @@ def gather_qmm(x: torch.Tensor, w: DeviceQTensor, indices: torch.Tensor,
     n = indices.numel()
     out = torch.empty(n, w.out, dtype=torch.bfloat16, device=x.device)
     l = _lib.load()
-    need = int(l.mrun_gather_qmm_workspace_bytes(n, w.experts))
+    need = int(l.mrun_gather_qmm_workspace_bytes(n, w.experts, x.shape[0], w.in_, w.out))
     ws = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
     qc = w.c
     check(l.mrun_gather_qmm(_ptr(x), x.shape[0], ctypes.byref(qc), _ptr(indices), n,
