@@ -108,7 +108,9 @@ int mrun_moe_forward(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t tok
  * chunks whose mrun_moe_workspace_bytes fits, e.g. a few hundred tokens of the Qwen3.6-like
  * block). A batch that needs more returns MRUN_ERR_WORKSPACE. The call allocates nothing; the
  * caller still passes x and out. Every call on one GPU shares that GPU's array, so calls that
- * overlap in time on one GPU (two streams, two threads) race: serialise them. */
+ * overlap in time on one GPU (two streams, two threads) race: serialise them.
+ * mrun_moe_forward_noalloc_max_bytes() also resolves the current GPU's scratch address; call it
+ * once on each GPU before capturing a graph, so that no call under capture looks up a symbol. */
 int mrun_moe_forward_noalloc(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t tokens,
                              mrun_bf16 *out, mrun_stream_t stream);
 size_t mrun_moe_forward_noalloc_max_bytes(void);

@@ -654,7 +654,12 @@ static Status scratch_of_current_device(void **ptr) {
 
 extern "C" {
 
-size_t mrun_moe_forward_noalloc_max_bytes(void) { return kScratchBytes; }
+size_t mrun_moe_forward_noalloc_max_bytes(void) {
+    void *p = nullptr;
+    (void)scratch_of_current_device(&p);  // the address lookup, outside any capture (errors: the
+                                          // forward reports them)
+    return kScratchBytes;
+}
 
 int mrun_moe_forward_noalloc(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t tokens,
                              mrun_bf16 *out, mrun_stream_t stream) {

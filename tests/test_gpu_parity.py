@@ -744,6 +744,27 @@ def test_null_biases_gather_qmm(q_host):
 
 
 # ---------------------------------------------------------------------------------------------
+# prefill with the routed experts on the grouped GEMM and the shared expert on the generic GEMMs
+
+@pytest.mark.parametrize("kind", ["wider_shared", "shared8"])
+@pytest.mark.parametrize("T", [64, 300])
+def test_shared_expert_on_generic_gemms(kind, T):
+    """The routed experts run the grouped GEMM (4-bit, group 64, widths multiples of 512) while the
+    shared expert cannot ride in its launches: a width unlike the routed one (1024 against 512),
+    or 8-bit shared projections of the routed width."""
+    if kind == "wider_shared":
+        shape = synth.Shape(hidden=2048, experts=64, top_k=8, intermediate=512, shared=1024)
+        hb = synth.make_block(shape, config=synth.CFG_PLUMBING, layer=T)
+    else:
+        shape = synth.Shape(hidden=2048, experts=64, top_k=8, intermediate=512, shared=512)
+        hb = synth.make_block(shape, config=synth.CFG_PLUMBING, layer=T + 1)
+        h8 = synth.make_block(shape, config=synth.CFG_PLUMBING, layer=T + 2, expert_bits=8)
+        hb.sh_gate_proj, hb.sh_up_proj, hb.sh_down_proj = h8.sh_gate_proj, h8.sh_up_proj, h8.sh_down_proj
+    dev = M.SparseMoe(hb)
+    run_block(hb, dev, synth.make_x(shape, T, config=synth.CFG_PLUMBING, layer=T), f"{kind} T={T}")
+
+
+# ---------------------------------------------------------------------------------------------
 # configs[3]: the 40-layer Qwen-shaped stack (weights generated on the device, 18 GB)
 
 N_STACK = 40

@@ -55,3 +55,40 @@ def test_noalloc_refuses_above_its_scratch():
         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     assert rc == _lib.MRUN_ERR_WORKSPACE
     assert b"scratch" in _lib.load().mrun_last_error()
+
+
+def test_noalloc_forwards_captured_in_a_graph():
+    """Noalloc forwards (decode T = 1, prefill T = 300) captured in a HIP graph: every replay, with
+    eager noalloc calls of another size in between (they overwrite the scratch array), equals
+    mrun_moe_forward bit for bit. The scratch address is resolved before the capture."""
+    hb = synth.make_block(synth.QWEN36, config=synth.CFG_DECODE, layer=902)
+    dev = M.SparseMoe(hb)
+    lib = _lib.load()
+    lib.mrun_moe_forward_noalloc_max_bytes()  # resolves this GPU's scratch address
+    for T, other in ((1, 300), (300, 1)):
+        x = M.bf16_tensor(synth.make_x(synth.QWEN36, T, config=synth.CFG_DECODE, layer=950 + T))
+        xo = M.bf16_tensor(synth.make_x(synth.QWEN36, other, config=synth.CFG_DECODE, layer=960))
+        want = M.bf16_bits(dev.forward(x))
+        out = torch.empty_like(x)
+
+        def call(stream):
+            _lib.check(lib.mrun_moe_forward_noalloc(
+                ctypes.byref(dev.c), ctypes.c_void_p(x.data_ptr()), T,
+                ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(stream.cuda_stream)))
+
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            call(s)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            call(torch.cuda.current_stream())
+        for rep in range(3):
+            out.zero_()
+            _noalloc(dev, xo)  # another size through the same scratch array
+            g.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(M.bf16_bits(out), want), f"T={T} replay {rep}"
+        print(f"noalloc T={T}: 3 graph replays bit-identical to mrun_moe_forward", flush=True)
