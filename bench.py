@@ -316,7 +316,38 @@ def calib_lib():
     lib.mrun_calib_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     lib.mrun_calib_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
                                     ctypes.c_void_p]
+    lib.mrun_calib_chain.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                     ctypes.c_void_p]
     return lib
+
+
+def launch_floor(torch, grids=(65, 576, 256), reps: int = 200) -> dict:
+    """The floor under the decode forward's three dependent launches: chains of three launches
+    with the T = 1 forward's grids (router, gate/up, down), each workgroup storing a word for the
+    next launch, timed like the forward (HIP events around `reps` back-to-back chains). `read`:
+    every thread of a launch first reads a word the previous launch wrote (one dependent global
+    read per launch, as each decode launch starts with one)."""
+    lib = calib_lib()
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    bufs = [torch.ones(max(grids) * 256, dtype=torch.int32, device="cuda") for _ in range(4)]
+    ptrs = (ctypes.c_void_p * 4)(*[b.data_ptr() for b in bufs])
+    g = (ctypes.c_int * 3)(*grids)
+    ev = Events(2)
+    res = {}
+    for read in (0, 1):
+        for _ in range(20):
+            assert lib.mrun_calib_chain(ptrs, g, read, sp) == 0
+        ev.record(0, stream)
+        for _ in range(reps):
+            assert lib.mrun_calib_chain(ptrs, g, read, sp) == 0
+        ev.record(1, stream)
+        res["read" if read else "empty"] = ev.ms(0, 1) * 1e3 / reps
+    return {"empty_us": res["empty"], "read_us": res["read"], "grids": list(grids),
+            "what": f"three dependent launches of {grids[0]}, {grids[1]} and {grids[2]} "
+                    f"workgroups x 256 threads (the T = 1 forward's grids), mean of {reps} "
+                    "back-to-back chains; read_us: each thread first reads a word the previous "
+                    "launch wrote"}
 
 
 class ColdTimer:
@@ -771,6 +802,7 @@ def main(argv=None) -> int:
     if not args.no_machine:
         print("[bench] copy and MFMA calibration", file=sys.stderr, flush=True)
         machine = machine_point(torch)
+        machine["launch_floor"] = launch_floor(torch)
 
     cpu = None
     if not args.no_cpu:

@@ -73,6 +73,17 @@ __global__ __launch_bounds__(256) void mfma_kernel(int iters, uint32_t pair,
 
 constexpr int kChains = 4;
 
+// One link of a chain of dependent launches: every thread reads one word that the previous launch
+// wrote (READ; a different word per workgroup, so the reads spread over the memory channels) and
+// stores one word for the next launch. The floor under a forward made of such launches.
+template <bool READ>
+__global__ __launch_bounds__(256) void chain_kernel(const uint32_t *__restrict__ src, int n_src,
+                                                    uint32_t *__restrict__ dst) {
+    uint32_t v = blockIdx.x;
+    if (READ) v += src[((size_t)blockIdx.x * 256 + threadIdx.x) % (size_t)n_src];
+    dst[(size_t)blockIdx.x * 256 + threadIdx.x] = v + 1;
+}
+
 }  // namespace
 
 extern "C" {
@@ -110,5 +121,19 @@ int mrun_calib_mfma(int blocks, int iters, float *out, void *stream) {
 }
 
 int mrun_calib_mfma_chains(void) { return kChains; }
+
+// Three dependent launches of g[0], g[1], g[2] workgroups of 256 threads: launch i reads (with
+// `read`) buf[i], the words launch i - 1 wrote (buf[0]: g[0] * 256 words the caller provides),
+// and writes buf[i + 1]; buf[i + 1] holds g[i] * 256 words.
+int mrun_calib_chain(uint32_t *const *buf, const int *g, int read, void *stream) {
+    if (!buf || !g) return (int)hipErrorInvalidValue;
+    for (int i = 0; i < 3; ++i) {
+        if (g[i] <= 0 || !buf[i] || !buf[i + 1]) return (int)hipErrorInvalidValue;
+        const int n_src = (i == 0 ? g[0] : g[i - 1]) * 256;
+        if (read) chain_kernel<true><<<g[i], 256, 0, (hipStream_t)stream>>>(buf[i], n_src, buf[i + 1]);
+        else chain_kernel<false><<<g[i], 256, 0, (hipStream_t)stream>>>(buf[i], n_src, buf[i + 1]);
+    }
+    return (int)hipGetLastError();
+}
 
 }  // extern "C"

@@ -23,6 +23,9 @@ pytestmark = pytest.mark.gpu
 
 SMALL = synth.Shape(hidden=256, experts=16, top_k=4, intermediate=128, shared=128)
 Q = synth.QWEN36
+# configs[3] deep layers: the largest share of a layer's elements that may differ from the oracle
+# by more than the north star's 2e-2 (each of them still within two bf16 ulps of its largest term)
+STACK_WIDE_SHARE = 1e-2
 
 
 def _log(*a):
@@ -841,8 +844,11 @@ def _stack_bar(got, ref, trace, label):
     mag = np.maximum(np.maximum(np.abs(g), np.abs(r)), terms)
     bound = np.maximum(2e-2, 2 * bf16_ulp(mag))
     s = stats(got, ref)
+    # the widened allowance is for the few elements whose terms are large: bound how many use it
+    s["beyond_2e-2"] = float(np.mean(np.abs(g - r) > 2e-2))
     assert np.all(np.abs(g - r) <= bound), f"{label}: {s}"
     assert s["l1_rel"] <= 1e-3, f"{label}: {s}"
+    assert s["beyond_2e-2"] <= STACK_WIDE_SHARE, f"{label}: {s}"
     return s
 
 
@@ -852,7 +858,7 @@ def _check_stack_layers(layers, trace, final, label):
     as a top-k within ties), and the residual add bit-exact. A 40-layer chain compounds one-ulp
     roundings (a residual value one ulp off changes the next norm and so the next routing), so
     the per-layer check is the bar."""
-    worst = None
+    worst, wide = None, 0.0
     for l, layer in enumerate(layers):
         x_l, h_l, o_l, ids = trace[l]
         assert ulp_distance(h_l, O.rms_norm(x_l, None, 1e-6)).max() <= 1, f"{label} layer {l} norm"
@@ -865,7 +871,9 @@ def _check_stack_layers(layers, trace, final, label):
         assert np.array_equal(nxt, O.bf16_from_f32(synth.bf16_to_f32(x_l) + synth.bf16_to_f32(o_l))), \
             f"{label} layer {l} residual"
         worst = s if worst is None or s["l1_rel"] > worst["l1_rel"] else worst
+        wide = max(wide, s["beyond_2e-2"])
         del hb
+    _log(f"{label}: largest share of a layer's elements beyond 2e-2: {wide:.2e}")
     return worst
 
 
