@@ -17,14 +17,13 @@ __device__ __forceinline__ void split3(float x, uint32_t &hi, uint32_t &mid, uin
     lo = __float_as_uint(r1 - m) >> 16;
 }
 
-// One 8-element block of a row: re-paired into its packed position, and its group's sum (the 8
-// blocks of a group are 8 aligned consecutive lanes) split into the three bf16.
+// One 8-element block v of a row (block blk): re-paired into its packed position, and its group's
+// sum (the 8 blocks of a group are 8 aligned consecutive lanes) split into the three bf16.
 // (store = false: the lane only takes part in the group sum)
-__device__ __forceinline__ void pack_block(const bf16_t *__restrict__ x, int lda, int row,
-                                           bool store, int K, int blk, bf16_t *__restrict__ xp,
-                                           int ldp, bf16_t *__restrict__ xs) {
+__device__ __forceinline__ void pack_block_v(uint4 v, int row, bool store, int K, int blk,
+                                             bf16_t *__restrict__ xp, int ldp,
+                                             bf16_t *__restrict__ xs) {
     const int g = blk >> 3, w = blk & 7;
-    const uint4 v = *(const uint4 *)(x + (size_t)row * lda + (size_t)blk * 8);
     const uint4 p = make_uint4(__builtin_amdgcn_perm(v.z, v.x, 0x05040100u),
                                __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
                                __builtin_amdgcn_perm(v.w, v.y, 0x05040100u),
@@ -45,6 +44,13 @@ __device__ __forceinline__ void pack_block(const bf16_t *__restrict__ x, int lda
         d[G] = (bf16_t)mid;
         d[2 * G] = (bf16_t)lo;
     }
+}
+
+__device__ __forceinline__ void pack_block(const bf16_t *__restrict__ x, int lda, int row,
+                                           bool store, int K, int blk, bf16_t *__restrict__ xp,
+                                           int ldp, bf16_t *__restrict__ xs) {
+    pack_block_v(*(const uint4 *)(x + (size_t)row * lda + (size_t)blk * 8), row, store, K, blk, xp,
+                 ldp, xs);
 }
 
 }  // namespace mrun

@@ -33,19 +33,19 @@ constexpr int kMaxT = 16, kMaxP = 128;
 // (bit p: pair p reads A row p / a_div and writes output row p). The next pair's activations are
 // loaded while the current pair is computed.
 // FULL: every row of the wave and every chunk of its lanes is in range (no masking).
-template <int LPR, int CPL, int RG, bool GLU, bool FULL = false>
+template <int LPR, int CPL, int RG, bool GLU, bool FULL = false, int B = 4>
 __device__ __forceinline__ void gemv_wave(const QW &w0, const QW &w1, int e, int row_base,
                                           const bf16_t *A, int lda, int a_div, uint64_t pm0,
                                           uint64_t pm1, bf16_t *out, int ldo, int lane) {
     constexpr int RPI = 64 / LPR;
     const int li = lane % LPR, rsub = lane / LPR;
     const int n_ch = w0.in >> 5;
-    WRow<CPL> r0[RG], r1[RG];
+    WRow<CPL, B> r0[RG], r1[RG];
 #pragma unroll
     for (int g = 0; g < RG; ++g) {
         const int row = row_base + g * RPI + rsub;
-        load_wrow<CPL>(w0, e, row, li, LPR, r0[g]);
-        if (GLU) load_wrow<CPL>(w1, e, row, li, LPR, r1[g]);
+        load_wrow<CPL, B>(w0, e, row, li, LPR, r0[g]);
+        if (GLU) load_wrow<CPL, B>(w1, e, row, li, LPR, r1[g]);
     }
     auto next = [&](uint64_t &m0, uint64_t &m1) -> int {
         if (m0) {
@@ -68,7 +68,7 @@ __device__ __forceinline__ void gemv_wave(const QW &w0, const QW &w1, int e, int
         const int pn = next(pm0, pm1);
         load_xrow_raw<CPL>(A + (size_t)((pn >= 0 ? pn : p) / a_div) * lda, li, LPR, n_ch, nxt);
         XChunk xc[CPL];
-        pair_xrow<CPL>(cur, xc);
+        pair_xrow<CPL, B>(cur, xc);
 #pragma unroll
         for (int g = 0; g < RG; ++g) {
             opaque_row(r0[g]);
@@ -92,7 +92,7 @@ __device__ __forceinline__ void gemv_wave(const QW &w0, const QW &w1, int e, int
             const int row = row_base + lane;
             if (lane < RG && row < w0.out) {
                 const float gt = rbf(a0), up = rbf(a1);
-                out[(size_t)p * ldo + paired_index(row)] = (bf16_t)f2bf((gt * sigmoidf_(gt)) * up);
+                out[(size_t)p * ldo + paired_index_b<B>(row)] = (bf16_t)f2bf((gt * sigmoidf_(gt)) * up);
             }
         } else {
 #pragma unroll
@@ -106,7 +106,7 @@ __device__ __forceinline__ void gemv_wave(const QW &w0, const QW &w1, int e, int
                         const float gt = rbf(a0), up = rbf(a1);
                         v = (gt * sigmoidf_(gt)) * up;
                     }
-                    out[(size_t)p * ldo + paired_index(row)] = (bf16_t)f2bf(v);
+                    out[(size_t)p * ldo + paired_index_b<B>(row)] = (bf16_t)f2bf(v);
                 }
             }
         }
@@ -507,7 +507,7 @@ __host__ __device__ inline int shared_gateup_blocks(const DecodeJob &j, int rows
 // it ran 2, and T = 1 took 4 us longer on the Coder shape)
 // FULL: D is exactly LPR * CPL chunks of 32 (rows are whole by construction: I and S are
 // multiples of the rows per workgroup).
-template <int LPR, int CPL, int RG, int NW, bool LOOP, bool SH_LAST, bool FULL = false>
+template <int LPR, int CPL, int RG, int NW, bool LOOP, bool SH_LAST, bool FULL = false, int B = 4>
 __global__ __launch_bounds__(64 * NW)
 __attribute__((amdgpu_waves_per_eu(LOOP && CPL == 3 ? 3 : 1))) void decode_gateup_kernel(
     DecodeJob j) {
@@ -601,15 +601,15 @@ __attribute__((amdgpu_waves_per_eu(LOOP && CPL == 3 ? 3 : 1))) void decode_gateu
                                    out + (size_t)p * ldo, lane);
         }
     } else {
-        gemv_wave<LPR, CPL, RG, true, FULL>(w0, w1, e, (rb * NW + wave) * RG * RPI, j.x, j.D,
-                                            a_div, pm0, pm1, out, ldo, lane);
+        gemv_wave<LPR, CPL, RG, true, FULL, B>(w0, w1, e, (rb * NW + wave) * RG * RPI, j.x, j.D,
+                                               a_div, pm0, pm1, out, ldo, lane);
     }
 }
 
 // ---------------------------------------------------------------------------------------------
 // K3: down + combine
 
-template <int LPR, int CPL, int SLPR, int SCPL, int PB, int kDownRowsPerWG>
+template <int LPR, int CPL, int SLPR, int SCPL, int PB, int kDownRowsPerWG, int B = 4>
 __global__ __launch_bounds__(256) void decode_down_kernel(DecodeJob j) {
     constexpr int RPI = 64 / LPR, NRG = kDownRowsPerWG / RPI;
     constexpr int SRPI = 64 / SLPR, SNRG = kDownRowsPerWG / SRPI, SG = (SNRG + 3) / 4;
@@ -631,7 +631,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeJob j) {
     const int P = j.T * j.k;
     const uint32_t my_id = j.ids[min((int)threadIdx.x, P - 1)];
     const uint32_t my_sc = j.scores[min((int)threadIdx.x, P - 1)];
-    WRow<SCPL> sr[SG];
+    WRow<SCPL, B> sr[SG];
     const int sli = lane % SLPR;
     XRaw scur[SCPL];
     {
@@ -650,7 +650,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeJob j) {
 #pragma unroll
         for (int i = 0; i < SG; ++i) {
             const int g = wave + 4 * i;
-            load_wrow<SCPL>(sd, 0, g < SNRG ? d0 + g * SRPI + lane / SLPR : j.D, sli, SLPR, sr[i]);
+            load_wrow<SCPL, B>(sd, 0, g < SNRG ? d0 + g * SRPI + lane / SLPR : j.D, sli, SLPR, sr[i]);
         }
         load_xrow_raw<SCPL>(has_s ? j.sh_act + (size_t)t0 * j.S : j.act, sli, SLPR,
                             (has_s ? j.S : j.I) >> 5, scur);
@@ -680,13 +680,13 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeJob j) {
     // takes PB pairs at a time and issues all their loads before computing
     for (int pb = p_lo; pb < p_hi; pb += PB) {
         if (pb != p_lo) load_act(pb);
-        WRow<CPL> wr[PB][NRG];
+        WRow<CPL, B> wr[PB][NRG];
 #pragma unroll
         for (int b = 0; b < PB; ++b) {
             const int e = (int)sid[min(pb + b, p_hi - 1)];
 #pragma unroll
             for (int g = 0; g < NRG; ++g)
-                load_wrow<CPL>(j.wd, e, d0 + g * RPI + rsub, li, LPR, wr[b][g]);
+                load_wrow<CPL, B>(j.wd, e, d0 + g * RPI + rsub, li, LPR, wr[b][g]);
         }
 #pragma unroll
         for (int b = 0; b < PB; ++b) {
@@ -839,7 +839,7 @@ static void launch_k1(const DecodeJob &j, hipStream_t s) {
     }
 }
 
-template <int LPR, int CPL, int PB, int DR>
+template <int LPR, int CPL, int PB, int DR, int B>
 static void launch_k3_pb(const DecodeJob &j, hipStream_t s);
 
 // K3 token groups: from T = 2 the tokens are split into groups, each with its own workgroups for
@@ -858,7 +858,7 @@ static int k3_token_groups(int T) { return T >= 8 ? 4 : (T >= 2 ? 2 : 1); }
 // rounds and had one block's loads in flight at a time. (On the 6144 x 2560 Coder shape this is 8
 // row blocks at T = 1 to 16; caps of 512, 2048 and 4096 per token measured slower.) Narrower rows
 // (one round already) take one row block per workgroup (the loop measured slower there).
-template <int RG, int NW, bool LOOP>
+template <int RG, int NW, bool LOOP, int B>
 static void launch_k2_l(const DecodeJob &j, int n_ch, dim3 g2, hipStream_t s) {
     auto go1 = [&](auto kernel) { kernel<<<g2, 64 * NW, 0, s>>>(j); };
     // the shared expert's workgroups last at T <= 2 (T = 1: 14.9 -> 14.2 us per block, T = 2:
@@ -869,6 +869,11 @@ static void launch_k2_l(const DecodeJob &j, int n_ch, dim3 g2, hipStream_t s) {
     };
     // whole rows of 2048 from T = 2: the unmasked row math (T = 16 59.3 -> 58.15 us per block,
     // T = 4 25.75 -> 25.55, T = 2 18.15 -> 18.0; at T = 1 within the noise)
+    if constexpr (B == 8) {  // 8-bit experts: rows of at most 2048 (one chunk per lane)
+        if (n_ch == 64 && (RG == 4 || j.T == 2)) go(decode_gateup_kernel<64, 1, RG, NW, false, false, true, 8>, decode_gateup_kernel<64, 1, RG, NW, false, true, true, 8>);
+        else go(decode_gateup_kernel<64, 1, RG, NW, false, false, false, 8>, decode_gateup_kernel<64, 1, RG, NW, false, true, false, 8>);
+        return;
+    }
     if (n_ch == 64 && !LOOP && (RG == 4 || j.T == 2)) go(decode_gateup_kernel<64, 1, RG, NW, false, false, true>, decode_gateup_kernel<64, 1, RG, NW, false, true, true>);
     else if (n_ch <= 64) go(decode_gateup_kernel<64, 1, RG, NW, LOOP, false>, decode_gateup_kernel<64, 1, RG, NW, LOOP, true>);
     else if (n_ch <= 128) go(decode_gateup_kernel<64, 2, RG, NW, LOOP, false>, decode_gateup_kernel<64, 2, RG, NW, LOOP, true>);
@@ -876,7 +881,7 @@ static void launch_k2_l(const DecodeJob &j, int n_ch, dim3 g2, hipStream_t s) {
     else go(decode_gateup_kernel<64, 4, RG, NW, LOOP, false>, decode_gateup_kernel<64, 4, RG, NW, LOOP, true>);
 }
 
-template <int RG, int NW>
+template <int RG, int NW, int B>
 static void launch_k2(DecodeJob j, int n_ch, hipStream_t s) {
     const int per_slot = j.I / (NW * RG), sh_blocks = j.S / (NW * RG);
     int L = 1;
@@ -885,11 +890,11 @@ static void launch_k2(DecodeJob j, int n_ch, hipStream_t s) {
         L *= 2;
     j.gu_loop = L;
     dim3 g2(shared_gateup_blocks(j, NW * RG * L) + (j.I / (NW * RG * L)) * j.max_slots);
-    if (RG == 1 && L > 1) launch_k2_l<1, NW, true>(j, n_ch, g2, s);
-    else launch_k2_l<RG, NW, false>(j, n_ch, g2, s);
+    if (RG == 1 && L > 1) launch_k2_l<1, NW, true, B>(j, n_ch, g2, s);
+    else launch_k2_l<RG, NW, false, B>(j, n_ch, g2, s);
 }
 
-template <int LPR, int CPL>
+template <int LPR, int CPL, int B>
 static void launch_k3_s(DecodeJob j, hipStream_t s) {
     j.down_tokens = (j.T + k3_token_groups(j.T) - 1) / k3_token_groups(j.T);
     // output rows per workgroup: two row groups per wave, at least 4 rows (8 with 16-lane rows,
@@ -902,20 +907,27 @@ static void launch_k3_s(DecodeJob j, hipStream_t s) {
     constexpr int DR = 2 * (64 / LPR) > 4 ? 2 * (64 / LPR) : 4;
     constexpr int NRG = DR / (64 / LPR) > 0 ? DR / (64 / LPR) : 1;
     constexpr int PB = (NRG * CPL <= 2) ? 4 : (NRG * CPL <= 4 ? 2 : 1);
-    if (j.T >= 8) launch_k3_pb<LPR, CPL, 1, DR>(j, s);
-    else if (PB == 4 && (j.down_tokens * j.k + 3) / 4 <= 8) launch_k3_pb<LPR, CPL, 2, DR>(j, s);
-    else launch_k3_pb<LPR, CPL, PB, DR>(j, s);
+    if (j.T >= 8) launch_k3_pb<LPR, CPL, 1, DR, B>(j, s);
+    else if (PB == 4 && (j.down_tokens * j.k + 3) / 4 <= 8) launch_k3_pb<LPR, CPL, 2, DR, B>(j, s);
+    else launch_k3_pb<LPR, CPL, PB, DR, B>(j, s);
 }
 
-template <int LPR, int CPL, int PB, int DR>
+template <int LPR, int CPL, int PB, int DR, int B>
 static void launch_k3_pb(const DecodeJob &j, hipStream_t s) {
     dim3 grid(j.D / DR * ((j.T + j.down_tokens - 1) / j.down_tokens));
     const int sch = j.S ? j.S >> 5 : 16;
-    if (sch == 16) decode_down_kernel<LPR, CPL, 16, 1, PB, DR><<<grid, 256, 0, s>>>(j);
-    else if (sch < 64) decode_down_kernel<LPR, CPL, 32, 2, PB, DR><<<grid, 256, 0, s>>>(j);
-    else if (sch <= 64) decode_down_kernel<LPR, CPL, 64, 1, PB, DR><<<grid, 256, 0, s>>>(j);
-    else if (sch <= 128) decode_down_kernel<LPR, CPL, 64, 2, PB, DR><<<grid, 256, 0, s>>>(j);
-    else decode_down_kernel<LPR, CPL, 64, 4, PB, DR><<<grid, 256, 0, s>>>(j);
+    if (sch == 16) decode_down_kernel<LPR, CPL, 16, 1, PB, DR, B><<<grid, 256, 0, s>>>(j);
+    else if (sch < 64) decode_down_kernel<LPR, CPL, 32, 2, PB, DR, B><<<grid, 256, 0, s>>>(j);
+    else if (sch <= 64 || B == 8) decode_down_kernel<LPR, CPL, 64, 1, PB, DR, B><<<grid, 256, 0, s>>>(j);
+    else if (sch <= 128) decode_down_kernel<LPR, CPL, 64, 2, PB, DR, B><<<grid, 256, 0, s>>>(j);
+    else decode_down_kernel<LPR, CPL, 64, 4, PB, DR, B><<<grid, 256, 0, s>>>(j);
+}
+
+// 8-bit experts take the same kernels with rows of at most 2048 inputs (one chunk of codes per
+// lane) and at most 2048 intermediate and shared outputs (the down kernel's chunk layouts)
+bool decode_supported_bits(int D, int I, int S, int bits) {
+    if (bits == 4) return true;
+    return bits == 8 && D <= 2048 && I <= 2048 && S <= 2048;
 }
 
 bool decode_supported(int D, int I, int S, int T, int k, int E) {
@@ -944,9 +956,12 @@ hipError_t launch_decode(const DecodeJob &j, hipStream_t s, StageMarks *marks) {
     // wider than 2048 take one row per wave and the streaming loop at every T
     const int rg = n_ch > 64 ? 1 : (j.T <= 2 ? 2 : 4);
     // 4 waves per workgroup: 8 and 16 (fewer redundant top-ks per CU) measured slower
-    if (rg == 1) launch_k2<1, 4>(j, n_ch, s);
-    else if (rg == 2) launch_k2<2, 4>(j, n_ch, s);
-    else launch_k2<4, 4>(j, n_ch, s);
+    const bool b8 = j.wg.bits == 8;
+    if (b8 && rg == 2) launch_k2<2, 4, 8>(j, n_ch, s);
+    else if (b8) launch_k2<4, 4, 8>(j, n_ch, s);
+    else if (rg == 1) launch_k2<1, 4, 4>(j, n_ch, s);
+    else if (rg == 2) launch_k2<2, 4, 4>(j, n_ch, s);
+    else launch_k2<4, 4, 4>(j, n_ch, s);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (marks) marks->mark(s);
@@ -956,12 +971,16 @@ hipError_t launch_decode(const DecodeJob &j, hipStream_t s, StageMarks *marks) {
         const dim3 g3(j.D / drs), b3(512);
         if (ich <= 128) decode_down_stream_kernel<2, kStreamBatch><<<g3, b3, 0, s>>>(j, drs);
         else decode_down_stream_kernel<3, kStreamBatch><<<g3, b3, 0, s>>>(j, drs);
-    } else if (ich == 16) launch_k3_s<16, 1>(j, s);
-    else if (ich < 64) launch_k3_s<32, 2>(j, s);
-    else if (ich <= 64) launch_k3_s<64, 1>(j, s);
-    else if (ich <= 128) launch_k3_s<64, 2>(j, s);
-    else if (ich <= 192) launch_k3_s<64, 3>(j, s);
-    else launch_k3_s<64, 4>(j, s);
+    } else if (b8) {  // 8-bit experts: I of at most 2048
+        if (ich == 16) launch_k3_s<16, 1, 8>(j, s);
+        else if (ich < 64) launch_k3_s<32, 2, 8>(j, s);
+        else launch_k3_s<64, 1, 8>(j, s);
+    } else if (ich == 16) launch_k3_s<16, 1, 4>(j, s);
+    else if (ich < 64) launch_k3_s<32, 2, 4>(j, s);
+    else if (ich <= 64) launch_k3_s<64, 1, 4>(j, s);
+    else if (ich <= 128) launch_k3_s<64, 2, 4>(j, s);
+    else if (ich <= 192) launch_k3_s<64, 3, 4>(j, s);
+    else launch_k3_s<64, 4, 4>(j, s);
     e = hipGetLastError();
     if (e == hipSuccess && marks) marks->mark(s);
     return e;

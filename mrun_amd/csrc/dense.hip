@@ -57,11 +57,27 @@ __global__ __launch_bounds__(256 * KG) void dense_gemm_kernel(DenseJob j) {
     if ((int)blockIdx.y >= nbw) {  // pack rows [64 x, +64) of K quarter y - nbw (apack's code)
         const int nq = dense_pack_quarters(j.K), kq = (int)blockIdx.y - nbw;
         const int bpr = j.K / nq / 8, r0 = (int)blockIdx.x * DBM;  // blocks per row and quarter
-        for (int i = threadIdx.x; i < DBM * bpr; i += 256 * KG) {
-            const int row = r0 + i / bpr, blk = kq * bpr + i % bpr;
-            // whole 64-lane waves take part in the DPP sum (bpr is a multiple of 8), rows past M
-            // are clamped for the loads and skipped for the stores
-            pack_block(j.A, j.lda, min(row, j.M - 1), row < j.M, j.K, blk, j.pack_a, j.K, j.pack_x);
+        // every thread takes the same number of blocks (DBM * bpr is a multiple of 512, since
+        // bpr is a multiple of 8), so whole 64-lane waves take part in each DPP sum; rows past M
+        // are clamped for the loads and skipped for the stores. The loads of PB blocks are issued
+        // before any is used: one round trip per PB blocks, not one per block.
+        constexpr int PB = 8;
+        const int step = 256 * KG;
+        for (int i0 = threadIdx.x; i0 < DBM * bpr; i0 += PB * step) {
+            uint4 v[PB];
+#pragma unroll
+            for (int u = 0; u < PB; ++u) {
+                const int i = min(i0 + u * step, DBM * bpr - 1);
+                const int row = r0 + i / bpr, blk = kq * bpr + i % bpr;
+                v[u] = *(const uint4 *)(j.A + (size_t)min(row, j.M - 1) * j.lda + (size_t)blk * 8);
+            }
+#pragma unroll
+            for (int u = 0; u < PB; ++u) {
+                const int i = i0 + u * step;
+                if (i >= DBM * bpr) break;  // uniform: the same count for every thread
+                const int row = r0 + i / bpr, blk = kq * bpr + i % bpr;
+                pack_block_v(v[u], min(row, j.M - 1), row < j.M, j.K, blk, j.pack_a, j.K, j.pack_x);
+            }
         }
         return;
     }

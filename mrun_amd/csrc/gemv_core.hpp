@@ -8,6 +8,13 @@
 //     sum_k x_k (q_k s + b) = s * sum_k x_k (128 + q_k) + (b - 128 s) * sum_k x_k.
 // A lane owns 32-code chunks li, li + LPR, ...; a chunk lies in one quant group (32 | group). The
 // LPR lanes of a row are summed by a fixed butterfly, so a row's bits depend on K only.
+//
+// 8-bit codes (B = 8; a chunk is two uint4): each byte's low and high nibble take the same bf16
+// trick, so a word of four codes gives the pairs (lo q_i, lo q_{i+2}), (lo q_{i+1}, lo q_{i+3}) and
+// the same for the high nibbles; the activations are re-paired as (x_i, x_{i+2}), (x_{i+1}, x_{i+3})
+// and with q = lo + 16 hi:
+//     sum_k x_k (q_k s + b) = s * (P'_lo + 16 P'_hi) + (b - 2176 s) * sum_k x_k,
+// P'_lo = sum x (128 + lo), P'_hi = sum x (128 + hi), 2176 = 128 * 17.
 #pragma once
 
 #include "common.hpp"
@@ -37,6 +44,23 @@ __device__ __forceinline__ void load_xraw(const bf16_t *src, XRaw &r) {
     const uint4 *p = (const uint4 *)src;
 #pragma unroll
     for (int w = 0; w < 4; ++w) r.a[w] = p[w];
+}
+
+// 32 activations re-paired for 8-bit codes, the order dot_chunk8 reads: dword 2i holds
+// (x[4i], x[4i+2]), dword 2i + 1 holds (x[4i+1], x[4i+3]); and their sum.
+__device__ __forceinline__ void pair_x8(const XRaw &r, XChunk &c) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint4 a = r.a[w];
+        c.v[4 * w + 0] = __builtin_amdgcn_perm(a.y, a.x, 0x05040100u);  // x0, x2
+        c.v[4 * w + 1] = __builtin_amdgcn_perm(a.y, a.x, 0x07060302u);  // x1, x3
+        c.v[4 * w + 2] = __builtin_amdgcn_perm(a.w, a.z, 0x05040100u);  // x4, x6
+        c.v[4 * w + 3] = __builtin_amdgcn_perm(a.w, a.z, 0x07060302u);  // x5, x7
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s = dot2(c.v[i], 0x3F803F80u, s);
+    c.sum = s;
 }
 
 __device__ __forceinline__ void pair_x(const XRaw &r, XChunk &c) {
@@ -78,25 +102,43 @@ __device__ __forceinline__ float dot_chunk(const uint4 &q, const XChunk &x) {
     return acc;
 }
 
-// One weight row's chunks for one lane: codes and the raw bf16 scale and bias. Loads use clamped
-// addresses and are never followed by a use inside a condition, so all of a wave's loads are in
-// flight together; `ok` bit c masks the chunks that lie past the row or the matrix, bit 31 says
-// whether the weight has biases.
-template <int CPL>
+// sum_k x_k (128 + lo_k) and sum_k x_k (128 + hi_k) over the 32 codes of two uint4 (8-bit codes)
+__device__ __forceinline__ float2 dot_chunk8(const uint4 *q, const XChunk &x) {
+    const uint32_t w[8] = {q[0].x, q[0].y, q[0].z, q[0].w, q[1].x, q[1].y, q[1].z, q[1].w};
+    uint32_t cm, cx;
+    code_consts(cm, cx);
+    float lo = 0.f, hi = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        lo = dot2(x.v[2 * i], (w[i] & cm) | cx, lo);
+        lo = dot2(x.v[2 * i + 1], ((w[i] >> 8) & cm) | cx, lo);
+        hi = dot2(x.v[2 * i], ((w[i] >> 4) & cm) | cx, hi);
+        hi = dot2(x.v[2 * i + 1], ((w[i] >> 12) & cm) | cx, hi);
+    }
+    return make_float2(lo, hi);
+}
+
+// One weight row's chunks for one lane: codes (B / 4 uint4 per chunk) and the raw bf16 scale and
+// bias. Loads use clamped addresses and are never followed by a use inside a condition, so all of
+// a wave's loads are in flight together; `ok` bit c masks the chunks that lie past the row or the
+// matrix, bit 31 says whether the weight has biases.
+template <int CPL, int B = 4>
 struct WRow {
-    uint4 q[CPL];
+    static constexpr int kBits = B, kQ = B / 4;
+    uint4 q[CPL * kQ];
     uint32_t s[CPL], b[CPL];
     uint32_t ok;
 };
 
-template <int CPL>
+template <int CPL, int B = 4>
 __device__ __forceinline__ void load_wrow(const QW &w, int e, int row, int li, int lpr,
-                                          WRow<CPL> &r) {
+                                          WRow<CPL, B> &r) {
+    constexpr int QC = B / 4;  // uint4 of codes per chunk
     const int n_ch = w.in >> 5;
     const int gshift = __builtin_ctz((unsigned)w.group);  // groups of 32, 64 or 128
     const int groups = w.in >> gshift;
     const size_t rr = (size_t)e * w.out + min(row, w.out - 1);
-    const uint32_t *codes = w.codes + rr * (size_t)(w.in >> 3);
+    const uint32_t *codes = w.codes + rr * (size_t)(w.in * B / 32);
     // without biases the scales stand in, so the load is unconditional; row_part zeroes the term
     const bf16_t *biases = w.biases ? w.biases : w.scales;
     r.ok = w.biases ? 0x80000000u : 0u;
@@ -104,7 +146,8 @@ __device__ __forceinline__ void load_wrow(const QW &w, int e, int row, int li, i
     for (int c = 0; c < CPL; ++c) {
         const int ch = li + c * lpr;
         const int chc = min(ch, n_ch - 1);
-        r.q[c] = *(const uint4 *)(codes + (size_t)chc * 4);
+#pragma unroll
+        for (int u = 0; u < QC; ++u) r.q[c * QC + u] = *(const uint4 *)(codes + (size_t)chc * 4 * QC + 4 * u);
         const size_t gi = rr * groups + ((chc * 32) >> gshift);
         r.s[c] = w.scales[gi];
         r.b[c] = biases[gi];
@@ -114,29 +157,35 @@ __device__ __forceinline__ void load_wrow(const QW &w, int e, int row, int li, i
 
 // Lane's part of row . x over its chunks: s * sum x (128 + q) + (b - 128 s) * sum x. FULL: the
 // caller's shape puts every chunk and row in range, so the `ok` masks are all set (same values).
-template <int CPL, bool FULL = false>
-__device__ __forceinline__ float row_part(const WRow<CPL> &r, const XChunk *x) {
+template <int CPL, bool FULL = false, int B = 4>
+__device__ __forceinline__ float row_part(const WRow<CPL, B> &r, const XChunk *x) {
     float a = 0.f;
     const bool has_b = (r.ok >> 31) & 1u;
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
         const bool ok = FULL || ((r.ok >> c) & 1u);
         const float s = ok ? bf2f(r.s[c]) : 0.f;
-        const float bp = ok ? (has_b ? bf2f(r.b[c]) : 0.f) - 128.f * s : 0.f;
-        a += s * dot_chunk(r.q[c], x[c]) + bp * x[c].sum;
+        if constexpr (B == 8) {
+            const float bp = ok ? (has_b ? bf2f(r.b[c]) : 0.f) - 2176.f * s : 0.f;
+            const float2 lh = dot_chunk8(&r.q[2 * c], x[c]);
+            a += s * (lh.x + 16.f * lh.y) + bp * x[c].sum;
+        } else {
+            const float bp = ok ? (has_b ? bf2f(r.b[c]) : 0.f) - 128.f * s : 0.f;
+            a += s * dot_chunk(r.q[c], x[c]) + bp * x[c].sum;
+        }
     }
     return a;
 }
 
 // Keeps a row's raw loads opaque inside a loop, so their conversions are not hoisted next to the
 // loads (where a conversion would wait for the load before the loads that follow are issued).
-template <int CPL>
-__device__ __forceinline__ void opaque_row(WRow<CPL> &r) {
+template <int CPL, int B>
+__device__ __forceinline__ void opaque_row(WRow<CPL, B> &r) {
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
+    for (int c = 0; c < CPL * (B / 4); ++c)
         asm volatile("" : "+v"(r.q[c].x), "+v"(r.q[c].y), "+v"(r.q[c].z), "+v"(r.q[c].w));
-        asm volatile("" : "+v"(r.s[c]), "+v"(r.b[c]));
-    }
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) asm volatile("" : "+v"(r.s[c]), "+v"(r.b[c]));
 }
 
 // The lane's chunks of one activation row (clamped: chunks past the row are masked by the
@@ -148,10 +197,13 @@ __device__ __forceinline__ void load_xrow_raw(const bf16_t *row, int li, int lpr
     for (int c = 0; c < CPL; ++c) load_xraw(row + min(li + c * lpr, n_ch - 1) * 32, x[c]);
 }
 
-template <int CPL>
+template <int CPL, int B = 4>
 __device__ __forceinline__ void pair_xrow(const XRaw *raw, XChunk *x) {
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) pair_x(raw[c], x[c]);
+    for (int c = 0; c < CPL; ++c) {
+        if constexpr (B == 8) pair_x8(raw[c], x[c]);
+        else pair_x(raw[c], x[c]);
+    }
 }
 
 // Rows that one GEMV writes for another to read (the decode's gate/up activations) are stored
@@ -160,6 +212,13 @@ __device__ __forceinline__ void pair_xrow(const XRaw *raw, XChunk *x) {
 // 8w + i + 4).
 __host__ __device__ constexpr int paired_index(int e) {
     return (e & ~31) | (e & 24) | ((e & 3) << 1) | ((e >> 2) & 1);
+}
+// the same for chunks that 8-bit weights read (pair_x8's order: elements 4i + j at 4i + 2 (j % 2)
+// + j / 2, i.e. bits 0 and 1 of the index swapped)
+template <int B>
+__host__ __device__ constexpr int paired_index_b(int e) {
+    if constexpr (B == 8) return (e & ~3) | ((e & 1) << 1) | ((e >> 1) & 1);
+    else return paired_index(e);
 }
 
 // A chunk stored re-paired: the words as loaded, and their sum in pair_x's order (same bits).

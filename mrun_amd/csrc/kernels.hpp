@@ -149,6 +149,7 @@ struct DecodeJob {
     unsigned long long *clock;  // benchmark instrumentation (StageMarks::k2_clock), or null
 };
 bool decode_supported(int D, int I, int S, int T, int k, int E);
+bool decode_supported_bits(int D, int I, int S, int bits);
 hipError_t launch_decode(const DecodeJob &job, hipStream_t stream, StageMarks *marks);
 
 // MFMA bf16 grouped GEMM (prefill): rows at sorted positions grouped in tiles (routing.tiles) or,

@@ -322,16 +322,19 @@ static bool is_decode(const mrun_moe_config &c, int T) {
                             c.experts);
 }
 
-// The decode kernels stream 4-bit experts; 8-bit ones take the generic products.
+// The decode kernels stream 4-bit experts, and 8-bit ones of the shapes decode_supported_bits
+// takes; every routed and shared expert projection has the same width of codes.
 static bool is_decode(const mrun_sparse_moe &m, int T) {
     const mrun_moe_config &c = m.cfg;
-    bool four = m.switch_gate_proj.bits == 4 && m.switch_up_proj.bits == 4 &&
-                m.switch_down_proj.bits == 4;
+    const int bits = m.switch_gate_proj.bits;
+    bool same = (bits == 4 || bits == 8) && m.switch_up_proj.bits == bits &&
+                m.switch_down_proj.bits == bits;
     if (c.shared_intermediate > 0)
-        four = four && !m.shared_gate_proj.weight && !m.shared_up_proj.weight &&
-               !m.shared_down_proj.weight && m.shared_gate_proj.q.bits == 4 &&
-               m.shared_up_proj.q.bits == 4 && m.shared_down_proj.q.bits == 4;
-    return four && is_decode(c, T);
+        same = same && !m.shared_gate_proj.weight && !m.shared_up_proj.weight &&
+               !m.shared_down_proj.weight && m.shared_gate_proj.q.bits == bits &&
+               m.shared_up_proj.q.bits == bits && m.shared_down_proj.q.bits == bits;
+    return same && decode_supported_bits(c.hidden, c.intermediate, c.shared_intermediate, bits) &&
+           is_decode(c, T);
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -502,11 +502,25 @@ def q8_blocks():
 @pytest.mark.parametrize("kind", ["experts8", "gates8", "both8"])
 @pytest.mark.parametrize("T", [1, 3, 16, 40, 300])
 def test_8bit_weights_match_oracle(q8_blocks, kind, T):
-    """8-bit experts run the generic products (GEMV at T <= 16, MFMA GEMM above); an 8-bit router
-    and shared gate run before the decode launches (T <= 16) or as the prefill's first product."""
+    """8-bit experts run the decode kernels at T <= 16 (each byte's two nibbles dotted as two 4-bit
+    codes) and the generic MFMA GEMM above; an 8-bit router and shared gate are dequantized inside
+    the decode router launch (T <= 16) or run as the prefill's first product."""
     hb, dev = q8_blocks[kind]
     x_np = synth.make_x(Q8, T, config=synth.CFG_DECODE, layer=100 + T)
     run_block(hb, dev, x_np, f"{kind} T={T}")
+
+
+def test_8bit_experts_rows_keep_their_one_row_bits(q8_blocks):
+    """8-bit experts at decode: every row of a batch of up to 16 has its one-row bits, as with
+    4-bit experts (the same kernels; nuvec.rs:256-265)."""
+    hb, dev = q8_blocks["both8"]
+    x_np = synth.make_x(Q8, 16, config=synth.CFG_DECODE, layer=88)
+    batch = M.bf16_bits(dev.forward(M.bf16_tensor(x_np)))
+    for T in (3, 9):
+        assert np.array_equal(M.bf16_bits(dev.forward(M.bf16_tensor(x_np[:T]))), batch[:T])
+    for t in (0, 5, 15):
+        one = M.bf16_bits(dev.forward(M.bf16_tensor(x_np[t:t + 1])))
+        assert np.array_equal(one[0], batch[t]), f"row {t}"
 
 
 @pytest.mark.parametrize("group", [32, 128])
@@ -665,10 +679,11 @@ def test_forward_permutation_zipf_2048():
 
 
 def test_forward_permutation_8bit_small(q8_blocks):
-    """8-bit experts take the prefill schedule at every size: 24 pairs, the permutation anyway."""
+    """8-bit experts at the first prefill size (T = 17, 136 pairs; up to 16 tokens they take the
+    decode schedule, which needs no permutation): the forward's permutation anyway."""
     hb, dev = q8_blocks["experts8"]
-    x_np = synth.make_x(Q8, 3, config=synth.CFG_DECODE, layer=41)
-    check_forward_permutation(hb, dev, x_np, "8-bit experts forward permutation T=3")
+    x_np = synth.make_x(Q8, 17, config=synth.CFG_DECODE, layer=41)
+    check_forward_permutation(hb, dev, x_np, "8-bit experts forward permutation T=17")
 
 
 def test_block_coder_prefill_8192():
