@@ -659,13 +659,18 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
             x_state = 1;
         } else {
             // each 4 x 4 block (4 rows of a lane, 4 columns of a lane quad) is transposed within
-            // the quad, so every lane stores 4 adjacent columns of one row (8 bytes)
+            // the quad (every lane then holds 4 adjacent columns of one row), and lanes l, l ^ 4
+            // (the two quads of 8 adjacent columns) trade halves of two such blocks, so that every
+            // lane stores 8 adjacent columns of one row (16 bytes)
             const int q = fr & 3;
+            const bool hq = (fr & 4) != 0;  // keeps the odd block of each pair
+            typedef unsigned u32x4s __attribute__((ext_vector_type(4)));
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni) {
-                const int col4 = ci.n0 + (ni ? bro1 : bro0) + (fr & ~3);
+                const int col8 = ci.n0 + (ni ? bro1 : bro0) + (fr & ~7);
 #pragma unroll
-                for (int mi = 0; mi < 2; ++mi)
+                for (int mi = 0; mi < 2; ++mi) {
+                    uint2 w4[4];
 #pragma unroll
                     for (int b = 0; b < 4; ++b) {
                         const uint32_t p02 = f2bf2(acc[mi][ni][4 * b], acc[mi][ni][4 * b + 2]);
@@ -678,11 +683,23 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
                         const uint32_t B = __builtin_amdgcn_perm(hi_src, lo_src, 0x07060302u);  // row 2 + (q & 1)
                         // lanes q, q ^ 2: lanes 0, 1 complete rows 0, 1; lanes 2, 3 rows 2, 3
                         const uint32_t r2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)((q & 2) ? A : B), 0x4E, 0xF, 0xF, false);
-                        const uint2 w = (q & 2) ? make_uint2(r2, B) : make_uint2(A, r2);
-                        const int r = mi * 32 + 8 * b + 4 * fh + q;
-                        typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-                        __builtin_amdgcn_raw_buffer_store_b64(u32x2{w.x, w.y}, r_out, (r * ldo + col4) * 2, 0, 0);
+                        w4[b] = (q & 2) ? make_uint2(r2, B) : make_uint2(A, r2);
                     }
+#pragma unroll
+                    for (int bp = 0; bp < 2; ++bp) {
+                        const uint2 keep = hq ? w4[2 * bp + 1] : w4[2 * bp];
+                        const uint2 send = hq ? w4[2 * bp] : w4[2 * bp + 1];
+                        // lane ^ 4 within each row of 16 lanes: banks 0, 2 read lane + 4, banks 1, 3 lane - 4
+                        int rx = __builtin_amdgcn_update_dpp(0, (int)send.x, 0x104, 0xF, 0x5, false);
+                        rx = __builtin_amdgcn_update_dpp(rx, (int)send.x, 0x114, 0xF, 0xA, false);
+                        int ry = __builtin_amdgcn_update_dpp(0, (int)send.y, 0x104, 0xF, 0x5, false);
+                        ry = __builtin_amdgcn_update_dpp(ry, (int)send.y, 0x114, 0xF, 0xA, false);
+                        const u32x4s v = hq ? u32x4s{(uint32_t)rx, (uint32_t)ry, keep.x, keep.y}
+                                            : u32x4s{keep.x, keep.y, (uint32_t)rx, (uint32_t)ry};
+                        const int r = mi * 32 + 8 * (2 * bp + (hq ? 1 : 0)) + 4 * fh + q;
+                        __builtin_amdgcn_raw_buffer_store_b128(v, r_out, (r * ldo + col8) * 2, 0, 0);
+                    }
+                }
             }
         }
 #pragma unroll
@@ -727,6 +744,13 @@ bool moe_gemm_supported(const MoeGemmJob &j) {
     auto a_fits = [](long long rows, int lda) { return rows > 0 && rows * lda * 2 < (1LL << 32); };
     if (!a_fits(j.a_rows, j.lda) || (j.has_shared && !a_fits(j.sh.M, j.sh.lda))) return false;
     if (j.w0.out != j.N || (j.glu && j.w1.out != j.N)) return false;
+    // epilogue stores: 16 bytes per lane (down: 8 adjacent columns) or 4 (gate/up: a packed
+    // pair), at row offsets from the output's base
+    auto out_ok = [&](const bf16_t *p, int ldo) {
+        const int a = j.glu ? 2 : 8;  // elements per store
+        return p && ldo > 0 && ldo % a == 0 && ((uintptr_t)p & (uintptr_t)(2 * a - 1)) == 0;
+    };
+    if (!out_ok(j.out, j.ldo) || (j.has_shared && !out_ok(j.sh.out, j.sh.ldo))) return false;
     // X splits: one entry per group of x (gate/up) or of act (down)
     const int axe = j.K / 64;
     if (j.ax_e != axe) return false;
