@@ -743,6 +743,12 @@ bool moe_gemm_supported(const MoeGemmJob &j) {
     // A row offsets (row * lda * 2 bytes, through a buffer resource) are 32-bit
     auto a_fits = [](long long rows, int lda) { return rows > 0 && rows * lda * 2 < (1LL << 32); };
     if (!a_fits(j.a_rows, j.lda) || (j.has_shared && !a_fits(j.sh.M, j.sh.lda))) return false;
+    // A rows and the X splits go to LDS in 16-byte copies
+    auto a_aligned = [](const bf16_t *a, int lda, const bf16_t *ax) {
+        return a && ax && lda % 8 == 0 && ((uintptr_t)a & 15) == 0 && ((uintptr_t)ax & 15) == 0;
+    };
+    if (!a_aligned(j.A, j.lda, j.AX) || (j.has_shared && !a_aligned(j.sh.A, j.sh.lda, j.sh.AX)))
+        return false;
     if (j.w0.out != j.N || (j.glu && j.w1.out != j.N)) return false;
     // epilogue stores: 16 bytes per lane (down: 8 adjacent columns) or 4 (gate/up: a packed
     // pair), at row offsets from the output's base
