@@ -145,9 +145,10 @@ int64_t mrun_wall_clock_hz(void);
  * profilers; no counterpart in the reference, whose intermediate arrays are not observable). For
  * `tokens` rows, at[0..6) receive byte offsets into the workspace of: ids [tokens, k] u32 and
  * scores [tokens, k] bf16 (the router's choice, moe.rs:151-159), and, for a batch that runs the
- * prefill schedule (more than 16 tokens, or 8-bit or dense experts), the sorted dispatch of
- * SwitchGlu::forward (moe.rs:65-75): offsets [experts + 1], order, inverse and token [tokens*k].
- * They hold the last forward's values until the workspace is reused. */
+ * prefill schedule (more than 32 tokens; more than 16 with experts the decode kernels do not
+ * take), the sorted dispatch of SwitchGlu::forward (moe.rs:65-75): offsets [experts + 1], order,
+ * inverse and token [tokens*k]. They hold the last forward's values until the workspace is
+ * reused. */
 int mrun_moe_workspace_routing(const mrun_moe_config *cfg, int32_t tokens, size_t *at);
 
 /* The router of SparseMoe::forward (moe.rs:151-159): logits = gate.forward(x) (load.rs:294-306),

@@ -352,10 +352,58 @@ struct FusedNorm {
 // post (the layer stack): when the forward ends in the combine launch and its rows are at most
 // 2048 wide, that launch also takes the stack's residual add and next RMSNorm (post_done set, and
 // `out` is not written).
+// the largest batch that runs as decode-schedule chunks of at most 16 tokens
+constexpr int kChunkedDecodeMax = 32;
+
+// Workspace of a batch that runs as decode chunks: the whole batch's ids and scores where the
+// batch's own plan keeps them (mrun_moe_workspace_routing), then one chunk's workspace.
+static size_t chunk_ws_offset(const mrun_moe_config &c, int T) {
+    const Plan p = make_plan(c, T);
+    return p.scores + a256(2 * (size_t)T * c.top_k);
+}
+static bool runs_chunked(int T) { return T > 16 && T <= kChunkedDecodeMax; }
+// the batch runs the decode schedule (at most 16 tokens, or chunks of at most 16)
+static bool decode_schedule(const mrun_sparse_moe &m, int T) {
+    if (runs_chunked(T)) return is_decode(m, 16) && is_decode(m, T % 16 ? T % 16 : 16);
+    return is_decode(m, T);
+}
+static size_t forward_ws_bytes(const mrun_moe_config &c, int T) {
+    const size_t plain = make_plan(c, T).total;
+    if (!runs_chunked(T)) return plain;
+    const size_t chunked = chunk_ws_offset(c, T) + make_plan(c, 16).total;
+    return plain > chunked ? plain : chunked;
+}
+
+// ids_at / scores_at (decode schedule only): where the routing goes instead of the plan's arrays.
 static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int T, bf16_t *out,
                                  char *ws, size_t ws_bytes, hipStream_t s, Stages *stg = nullptr,
                                  const FusedNorm *fn = nullptr, const PostNorm *post = nullptr,
-                                 bool *post_done = nullptr) {
+                                 bool *post_done = nullptr, uint32_t *ids_at = nullptr,
+                                 bf16_t *scores_at = nullptr) {
+    // 17 to kChunkedDecodeMax tokens: the decode schedule on chunks of at most 16 tokens (the
+    // tokens of a chunk, then the rest), which streams each chunk's expert rows once, against the
+    // prefill schedule's 64-row tiles that are mostly padding at these sizes. Every token's row
+    // is computed alone as in any decode batch. Instrumented calls (stg) keep one schedule.
+    if (!stg && runs_chunked(T) && decode_schedule(m, T)) {
+        const mrun_moe_config &c = m.cfg;
+        const int D = c.hidden, k = c.top_k;
+        if (ws_bytes < forward_ws_bytes(c, T))
+            return Err(MRUN_ERR_WORKSPACE, "workspace of " + std::to_string(ws_bytes) +
+                                               " bytes, need " + std::to_string(forward_ws_bytes(c, T)));
+        const Plan p = make_plan(c, T);
+        const size_t off = chunk_ws_offset(c, T);
+        if (post_done) *post_done = false;
+        for (int t0 = 0; t0 < T; t0 += 16) {
+            const int tc = T - t0 < 16 ? T - t0 : 16;
+            FusedNorm f{};
+            if (fn) f = FusedNorm{fn->src + (size_t)t0 * D, fn->w, fn->eps};
+            TRY(sparse_moe_forward(m, x + (size_t)t0 * D, tc, out + (size_t)t0 * D, ws + off,
+                                   ws_bytes - off, s, nullptr, fn ? &f : nullptr, nullptr, nullptr,
+                                   (uint32_t *)(ws + p.ids) + (size_t)t0 * k,
+                                   (bf16_t *)(ws + p.scores) + (size_t)t0 * k));
+        }
+        return Ok();
+    }
     Stages none;
     Stages &st = stg ? *stg : none;
     if (st.events && st.n_events > 0) (void)hipEventRecord(st.events[0], s);
@@ -404,7 +452,8 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
             j.sd = qw_of(as_quantized(m.shared_down_proj));
         }
         j.logits = logits, j.sh_logit = sh_logit, j.sh_act = sh_act, j.act = act, j.out = out;
-        j.ids = ids, j.scores = scores, j.topk_in_kernel = T <= 4;
+        j.ids = ids_at ? ids_at : ids, j.scores = scores_at ? scores_at : scores;
+        j.topk_in_kernel = T <= 4;
         // a quantized router or shared gate (8-bit in mlx-community conversions): K1 dequantizes
         // its rows (4 or 8 bits; the checked group sizes keep a lane's 8-element chunks in one
         // group)
@@ -602,7 +651,7 @@ int mrun_moe_check(const mrun_sparse_moe *moe) { return report(check_block(moe))
 
 size_t mrun_moe_workspace_bytes(const mrun_moe_config *cfg, int32_t tokens) {
     if (!cfg || tokens <= 0 || !check_config(*cfg).ok()) return 0;
-    return make_plan(*cfg, tokens).total;
+    return models::forward_ws_bytes(*cfg, tokens);
 }
 
 int mrun_moe_forward(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t tokens,
@@ -673,7 +722,7 @@ int mrun_moe_forward_noalloc(const mrun_sparse_moe *moe, const mrun_bf16 *x, int
     if (st.ok()) st = check_ptr(out, "out");
     if (st.ok() && x == out) st = Err(MRUN_ERR_INVALID, "out must not alias x");
     if (st.ok()) {
-        const size_t need = make_plan(moe->cfg, tokens).total;
+        const size_t need = models::forward_ws_bytes(moe->cfg, tokens);
         if (need > kScratchBytes)
             st = Err(MRUN_ERR_WORKSPACE,
                      "forward_noalloc: " + std::to_string(tokens) + " tokens need " +
@@ -1019,8 +1068,9 @@ int mrun_moe_stack_forward(const mrun_sparse_moe *layers, int32_t n_layers,
         // decode-sized chunks with dense or 4/8-bit routers: the norm runs inside each block's
         // router launch and the residual add inside its last launch (three launches per layer,
         // no norm kernel)
-        bool fused = models::is_decode(layers[0], tokens) &&
-                     2 * (size_t)tokens * D <= 65536;  // the normalised rows fit the router's LDS
+        const int chunk = tokens < 16 ? tokens : 16;  // tokens per decode launch
+        bool fused = models::decode_schedule(layers[0], tokens) &&
+                     2 * (size_t)chunk * D <= 65536;  // the normalised rows fit the router's LDS
         for (int32_t l = 0; fused && l < n_layers; ++l)
             fused = models::k1_router_ok(layers[l].gate) &&
                     (c.shared_intermediate == 0 || models::k1_router_ok(layers[l].shared_expert_gate));

@@ -222,7 +222,7 @@ def test_block_plumbing_config(q_host, q_dev):
     run_block(q_host, q_dev, x_np, "Q configs[0] T=16")
 
 
-@pytest.mark.parametrize("T", [17, 64, 300])
+@pytest.mark.parametrize("T", [17, 33, 64, 300])
 def test_block_prefill_small(q_host, q_dev, T):
     x_np = synth.make_x(Q, T, config=synth.CFG_PREFILL_ZIPF, layer=T)
     run_block(q_host, q_dev, x_np, f"Q prefill T={T}")
@@ -252,14 +252,14 @@ def test_block_prefill_4096():
 
 
 def test_rows_keep_their_one_row_bits(q_dev):
-    """A decode batch of T <= 16 rows gives every row the bits of its one-row product
-    (with_row_exact, nuvec.rs:256-265; lanes.rs:68-112)."""
-    x_np = synth.make_x(Q, 16, config=synth.CFG_DECODE, layer=77)
+    """A decode batch of T <= 16 rows, and one of up to 32 rows (decode chunks of 16), gives every
+    row the bits of its one-row product (with_row_exact, nuvec.rs:256-265; lanes.rs:68-112)."""
+    x_np = synth.make_x(Q, 32, config=synth.CFG_DECODE, layer=77)
     batch = M.bf16_bits(q_dev.forward(M.bf16_tensor(x_np)))
-    for T in (8, 16):
+    for T in (8, 16, 17, 24):
         b = M.bf16_bits(q_dev.forward(M.bf16_tensor(x_np[:T])))
-        assert np.array_equal(b, batch[:T])
-    for t in range(16):
+        assert np.array_equal(b, batch[:T]), f"T={T}"
+    for t in list(range(16)) + [16, 23, 31]:
         one = M.bf16_bits(q_dev.forward(M.bf16_tensor(x_np[t:t + 1])))
         assert np.array_equal(one[0], batch[t]), f"row {t}"
 
@@ -435,11 +435,11 @@ def stack3_gates8():
     return hosts, M.MoeStack([M.SparseMoe(h) for h in hosts])
 
 
-@pytest.mark.parametrize("T", [4, 40])
+@pytest.mark.parametrize("T", [4, 24, 40])
 def test_stack_matches_layer_loop_and_oracle(stack3, T):
     """configs[3]'s decoder-layer loop, x = R(x + MoE_l(rms_norm(x))) per layer, with layer l's
-    residual add and layer l+1's norm fused (add_rms_norm). T=4 takes the decode schedule, T=40 the
-    prefill one. Bit-identical to the loop of single ops on the GPU. Against the CPU restatement,
+    residual add and layer l+1's norm fused (add_rms_norm). T=4 takes the decode schedule, T=24 the
+    decode schedule in chunks of 16 and 8 tokens, T=40 the prefill one. Bit-identical to the loop of single ops on the GPU. Against the CPU restatement,
     layer by layer on the GPU's expert choices (each validated as a top-k within ties): within the
     block bar plus one bf16 ulp of the residual stream (a rounding of x + MoE(h) that lands on the
     neighbouring value moves x by one ulp of |x|, which exceeds 2e-2 where |x| >= 4)."""
@@ -546,7 +546,7 @@ def test_quantized_linear_facade():
         assert beyond_rounding(got, ref) == 0, stats(got, ref)
 
 
-@pytest.mark.parametrize("T", [4, 40])
+@pytest.mark.parametrize("T", [4, 24, 40])
 def test_stack_graph_replays_match_eager(stack3, T):
     """The stack captured as one HIP graph (no memset nodes: counters are cleared by kernels):
     every replay, with eager work in between, equals the eager result."""
@@ -617,14 +617,19 @@ def test_config_edges(shape, Ts):
                   f"{shape.name} T={T}")
 
 
-def test_decode_boundary_t17(q_host, q_dev):
-    """T = 16 is the last decode size and T = 17 the first prefill one: the same token's output
-    agrees between them within the bar (the two schedules accumulate in different orders)."""
-    x17 = synth.make_x(Q, 17, config=synth.CFG_DECODE, layer=17)
-    a = M.bf16_bits(q_dev.forward(M.bf16_tensor(x17)))
-    b = M.bf16_bits(q_dev.forward(M.bf16_tensor(x17[:16])))
+def test_decode_boundary_t33(q_host, q_dev):
+    """T = 32 is the last size that runs as decode chunks and T = 33 the first prefill one: the same
+    token's output agrees between them within the bar (the two schedules accumulate in different
+    orders), and T = 17 (a chunk of 16, then one of 1) gives its rows the T = 16 bits."""
+    x33 = synth.make_x(Q, 33, config=synth.CFG_DECODE, layer=17)
+    a = M.bf16_bits(q_dev.forward(M.bf16_tensor(x33)))
+    b = M.bf16_bits(q_dev.forward(M.bf16_tensor(x33[:32])))
+    c = M.bf16_bits(q_dev.forward(M.bf16_tensor(x33[:17])))
+    d = M.bf16_bits(q_dev.forward(M.bf16_tensor(x33[:16])))
     torch.cuda.synchronize()
-    assert_close(b, a[:16], what="T=16 decode vs T=17 prefill rows")
+    assert_close(b, a[:32], what="T=32 decode chunks vs T=33 prefill rows")
+    assert np.array_equal(c[:16], d), "T=17 rows 0-15 against T=16"
+    assert_close(c, a[:17], what="T=17 decode chunks vs T=33 prefill rows")
 
 
 # ---------------------------------------------------------------------------------------------
@@ -664,7 +669,7 @@ def check_forward_permutation(hb, dev, x_np, label, check_rows=None):
     _log(f"{label}: permutation bit-exact ({T * k} pairs), {s}")
 
 
-@pytest.mark.parametrize("T", [17, 300])
+@pytest.mark.parametrize("T", [33, 300])
 def test_forward_permutation_q(q_host, q_dev, T):
     x_np = synth.make_x(Q, T, config=synth.CFG_PREFILL_ZIPF, layer=40 + T)
     check_forward_permutation(q_host, q_dev, x_np, f"Q forward permutation T={T}")
@@ -679,11 +684,11 @@ def test_forward_permutation_zipf_2048():
 
 
 def test_forward_permutation_8bit_small(q8_blocks):
-    """8-bit experts at the first prefill size (T = 17, 136 pairs; up to 16 tokens they take the
+    """8-bit experts at the first prefill size (T = 33, 264 pairs; up to 32 tokens they take the
     decode schedule, which needs no permutation): the forward's permutation anyway."""
     hb, dev = q8_blocks["experts8"]
-    x_np = synth.make_x(Q8, 17, config=synth.CFG_DECODE, layer=41)
-    check_forward_permutation(hb, dev, x_np, "8-bit experts forward permutation T=17")
+    x_np = synth.make_x(Q8, 33, config=synth.CFG_DECODE, layer=41)
+    check_forward_permutation(hb, dev, x_np, "8-bit experts forward permutation T=33")
 
 
 def test_block_coder_prefill_8192():
