@@ -792,6 +792,20 @@ def main(argv=None) -> int:
                                "tokens_per_s": T / (wall * 1e-3)}
         del d8, h8
 
+    # between the decode sizes and the prefill chunk: block time by batch size on the configs[1]
+    # block (unbiased router); up to 32 tokens the decode schedule runs in chunks of 16
+    batches = None
+    if not args.no_sweep:
+        print("[bench] batch sizes 17 to 1024", file=sys.stderr, flush=True)
+        batches = []
+        for T in (17, 24, 32, 33, 64, 128, 256, 512, 1024):
+            xb = M.bf16_tensor(synth.make_x(Q, T, config=synth.CFG_DECODE, layer=T))
+            wall, dev_ms, _ = time_forward(dev, xb, 50, 10, torch)
+            batches.append({"tokens": T, "device_ms": dev_ms, "ms_per_step": wall,
+                            "tokens_per_s": T / (wall * 1e-3),
+                            "schedule": "decode, chunks of 16" if T <= 32 else "prefill"})
+            del xb
+
     prefill = None if args.no_prefill else prefill_point(args, Q, M, synth, torch)
     facade = None if args.no_prefill else facade_point(args, Q, M, synth, torch)
     formats = None if args.no_sweep else formats_point(args, Q, M, synth, torch)
@@ -840,6 +854,7 @@ def main(argv=None) -> int:
         "machine": machine,
         "sweep": sweep,
         "gates8": gates8,
+        "batches": batches,
         "prefill": prefill,
         "facade": facade,
         "formats": formats,
