@@ -28,12 +28,12 @@ def _noalloc(dev, x):
     return out
 
 
-@pytest.mark.parametrize("shape,Ts", [(synth.QWEN36, (300, 4, 1)), (SMALL, (40, 3))])
+@pytest.mark.parametrize("shape,Ts", [(synth.QWEN36, (300, 24, 4, 1)), (SMALL, (40, 3))])
 def test_noalloc_matches_forward(shape, Ts):
     hb = synth.make_block(shape, config=synth.CFG_DECODE, layer=900)
     dev = M.SparseMoe(hb)
     cap = int(_lib.load().mrun_moe_forward_noalloc_max_bytes())
-    for T in Ts:  # prefill first, then smaller decode batches over its stale scratch contents
+    for T in Ts:  # prefill first, then smaller decode batches (24: two chunks) over stale scratch
         assert dev.workspace_bytes(T) <= cap
         x = M.bf16_tensor(synth.make_x(shape, T, config=synth.CFG_DECODE, layer=900 + T))
         want = M.bf16_bits(dev.forward(x))
