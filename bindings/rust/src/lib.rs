@@ -35,7 +35,8 @@ pub const MRUN_ERR_HIP: c_int = 4;
 /// `tensor::Quantized` (nuvec.rs:602-638): codes `[experts, out, in*bits/32]` u32 (LSB first,
 /// nuvec.rs:1199-1203), scales and biases `[experts, out, in/group_size]` bf16, biases null for
 /// zeros (nuvec.rs:609-626). bits 16: dense bf16 `[experts, out, in]` in `weight`
-/// (`SwitchLinear::Dense`, moe.rs:43-46).
+/// (`SwitchLinear::Dense`, moe.rs:43-46); bits 32: dense f32 the same way (an f32 block, run by
+/// `mrun_moe_forward_f32`).
 #[repr(C)]
 #[derive(Clone, Copy, Debug)]
 pub struct mrun_quantized {
@@ -111,6 +112,18 @@ extern "C" {
         x: *const mrun_bf16,
         tokens: i32,
         out: *mut mrun_bf16,
+        workspace: *mut c_void,
+        workspace_bytes: usize,
+        stream: mrun_stream_t,
+    ) -> c_int;
+    /// `SparseMoe::forward` of an f32 checkpoint's block: every weight dense f32 (bits 32),
+    /// x and out f32 (nuvec.rs:688-697 runs the dense gather_mm in f32).
+    pub fn mrun_moe_workspace_bytes_f32(cfg: *const mrun_moe_config, tokens: i32) -> usize;
+    pub fn mrun_moe_forward_f32(
+        moe: *const mrun_sparse_moe,
+        x: *const f32,
+        tokens: i32,
+        out: *mut f32,
         workspace: *mut c_void,
         workspace_bytes: usize,
         stream: mrun_stream_t,

@@ -50,7 +50,8 @@ enum {
  * A non-stacked weight (quantized_matmul) has experts = 1.
  * bits = 16 carries unquantized experts (SwitchLinear::Dense, moe.rs:43-46, run by gather_mm,
  * nuvec.rs:688-697): weight points to bf16 [experts, out, in], scales and biases are NULL and
- * group_size is ignored. */
+ * group_size is ignored. bits = 32 carries dense f32 weights the same way (weight -> float
+ * [experts, out, in]); only mrun_moe_forward_f32 runs them. */
 typedef struct mrun_quantized {
     const uint32_t *weight;
     const mrun_bf16 *scales;
@@ -88,7 +89,8 @@ const char *mrun_last_error(void);
 const char *mrun_version(void);
 
 /* Validates a block's configuration and weight shapes as SparseMoe::load does
- * (moe.rs:120-147, load.rs:14-156, qwen3_5_moe.rs:508-513). No device work. */
+ * (moe.rs:120-147, load.rs:14-156, qwen3_5_moe.rs:508-513); a block with f32 (bits 32) experts
+ * as mrun_moe_forward_f32 takes it. No device work. */
 int mrun_moe_check(const mrun_sparse_moe *moe);
 
 /* Workspace bytes mrun_moe_forward needs for `tokens` rows (the counterpart of
@@ -100,6 +102,19 @@ size_t mrun_moe_workspace_bytes(const mrun_moe_config *cfg, int32_t tokens);
 int mrun_moe_forward(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t tokens,
                      mrun_bf16 *out, void *workspace, size_t workspace_bytes,
                      mrun_stream_t stream);
+
+/* SparseMoe::forward (moe.rs:149-174) for a block whose tensors are all float32, as the reference
+ * runs an f32 checkpoint: its Hugging Face fixture is f32 (gen_tiny.py:235-274) because MLX runs
+ * the dense gather_mm (nuvec.rs:688-697) only in f32, and every op of the block then computes and
+ * keeps f32. Every weight is dense f32 with bits = 32: the experts as mrun_quantized (weight ->
+ * float [experts, out, in], scales and biases NULL), each Linear in its `q` (experts 1, `weight`
+ * and `bias` NULL). x, out [tokens, hidden] float; out must not alias x. The op sequence is
+ * mrun_moe_forward's without its bf16 roundings: f32 softmax, top-k with equal gates ranked by
+ * lower id, SwiGLU, the weighted combine (pairs in rank order) and the sigmoid-gated shared
+ * expert. mrun_moe_forward refuses bits-32 weights with MRUN_ERR_UNSUPPORTED. */
+size_t mrun_moe_workspace_bytes_f32(const mrun_moe_config *cfg, int32_t tokens);
+int mrun_moe_forward_f32(const mrun_sparse_moe *moe, const float *x, int32_t tokens, float *out,
+                         void *workspace, size_t workspace_bytes, mrun_stream_t stream);
 
 /* mrun_moe_forward for callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). It has no counterpart in the reference.

@@ -76,6 +76,11 @@ SIGNATURES = {
         c_int32,
         [POINTER(SparseMoe), c_void_p, c_int32, c_void_p, c_void_p, c_size_t, c_void_p],
     ),
+    "mrun_moe_workspace_bytes_f32": (c_size_t, [POINTER(MoeConfig), c_int32]),
+    "mrun_moe_forward_f32": (
+        c_int32,
+        [POINTER(SparseMoe), c_void_p, c_int32, c_void_p, c_void_p, c_size_t, c_void_p],
+    ),
     "mrun_moe_forward_noalloc": (
         c_int32, [POINTER(SparseMoe), c_void_p, c_int32, c_void_p, c_void_p],
     ),

@@ -25,7 +25,7 @@ LIB = PKG / "lib"
 OBJ = PKG / "_build"
 INCLUDE = ROOT / "include"
 
-HIP_SOURCES = ["router.hip", "decode.hip", "qgemv.hip", "qgemm.hip", "moe_gemm.hip", "dense.hip",
+HIP_SOURCES = ["router.hip", "decode.hip", "qgemv.hip", "qgemm.hip", "moe_gemm.hip", "dense.hip", "f32.hip",
                "elementwise.hip", "moe.cpp", "loader.cpp"]
 ARCH = os.environ.get("MRUN_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -284,4 +284,26 @@ hipError_t launch_fill_u32(uint32_t *dst, uint32_t v, int n, hipStream_t stream)
 hipError_t launch_rows_gather(const bf16_t *src, const uint32_t *map, int rows, int width,
                               bf16_t *dst, hipStream_t stream);
 
+// ---- float32 blocks (f32.hip): every op in f32, nothing rounded to bf16 ----
+
+// out[r][n] = A[r / a_div] . W0[e_r][n] (e_r = ids ? ids[r] : 0), r < R, n < N, over K (a multiple
+// of 4, 16-byte aligned rows); with glu, silu(A . W0[e_r][n]) * (A . W1[e_r][n]). W [experts][N][K].
+struct F32Rows {
+    const float *A;
+    int a_div, K;
+    const float *W0, *W1;
+    const uint32_t *ids;
+    int R, N;
+    float *out;
+};
+hipError_t launch_f32_rows(const F32Rows &j, bool glu, hipStream_t stream);
+// softmax (f32) and top-k of T tokens (E <= 512; equal gates: lower id first; rank order); scores
+// are the gates, divided by their sum (in rank order) with norm
+hipError_t launch_f32_topk(const float *logits, int T, int E, int k, bool norm, uint32_t *ids,
+                           float *scores, hipStream_t stream);
+// out = sum_j y[t k + j] * scores[t k + j] (+ sigmoid(glogit[t]) * shared[t] when shared is set)
+hipError_t launch_f32_combine(const float *y, const float *scores, int T, int k, int D,
+                              const float *glogit, const float *shared, float *out,
+                              hipStream_t stream);
+
 }  // namespace mrun

@@ -579,13 +579,18 @@ static Status check_linear(const HostLinear &l, int experts, int out, int in, bo
     };
     if (l.bias && !allow_bias) return invalid("weights", l.path + ".bias is not supported");
     if (!l.quantized) {
-        if (stacked && l.weight->dtype != "BF16")
+        // dense bf16, or f32 (an f32 checkpoint's block runs through mrun_moe_forward_f32)
+        const bool f32 = l.weight->dtype == "F32";
+        if (stacked && l.weight->dtype != "BF16" && !f32)
             return Err(MRUN_ERR_UNSUPPORTED,
                        l.path + ": dense " + l.weight->dtype + " " + shape_str(l.weight->shape) +
-                           " experts (gather_mm) are not run by this build (bf16 only)");
-        if (l.weight->dtype != "BF16")
+                           " experts (gather_mm) are not run by this build (bf16 or f32 only)");
+        if (l.weight->dtype != "BF16" && !f32)
             return Err(MRUN_ERR_UNSUPPORTED, l.path + ": dense " + l.weight->dtype +
-                                                 " weights are not run by this build (bf16 only)");
+                                                 " weights are not run by this build (bf16 or "
+                                                 "f32 only)");
+        if (f32 && l.bias)
+            return Err(MRUN_ERR_UNSUPPORTED, l.path + ".bias: f32 Linear biases are not run");
         if (l.weight->shape != want({out, in}))
             return invalid("weights", l.path + ".weight: shape " + shape_str(l.weight->shape) +
                                           ", expected " + shape_str(want({out, in})));
@@ -643,11 +648,15 @@ static Status to_device(mrun_weights &w, const HostLinear &l, int experts, int o
         v.experts = experts, v.out = out, v.in = in, v.group_size = l.q.group_size, v.bits = l.q.bits;
         if (q) *q = v;
         if (lin) lin->q = v;
-    } else if (q) {  // dense bf16 experts: a 16-bit stacked weight (gather_mm)
+    } else if (q || l.weight->dtype == "F32") {
+        // dense experts (gather_mm) as a 16-bit (bf16) or 32-bit (f32) stacked weight; an f32
+        // Linear carries its weight the same way, in its `q`
         TRY(upload(w, *l.weight, &p));
         mrun_quantized v{};
-        v.weight = (const uint32_t *)p, v.experts = experts, v.out = out, v.in = in, v.bits = 16;
-        *q = v;
+        v.weight = (const uint32_t *)p, v.experts = experts, v.out = out, v.in = in;
+        v.bits = l.weight->dtype == "F32" ? 32 : 16;
+        if (q) *q = v;
+        if (lin) lin->q = v;
     } else {
         TRY(upload(w, *l.weight, &p));
         lin->weight = (const mrun_bf16 *)p;

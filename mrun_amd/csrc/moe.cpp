@@ -43,6 +43,10 @@ static QW qw_of(const mrun_quantized &q) {
 
 static Status check_quantized(const mrun_quantized *q, const std::string &path, int experts,
                               int out, int in) {
+    if (q && q->bits == 32)
+        return Err(MRUN_ERR_UNSUPPORTED,
+                   path + ": f32 weights (bits 32) run through mrun_moe_forward_f32, whose block "
+                          "is f32 throughout");
     if (q && q->bits == 16) {  // dense bf16 experts (SwitchLinear::Dense, moe.rs:43-46)
         if (!q->weight) return Err(MRUN_ERR_INVALID, path + ": missing tensors");
         if (q->scales || q->biases)
@@ -158,6 +162,10 @@ static Status check_block(const mrun_sparse_moe *m) {
         else TRY(check_quantized(&m->shared_expert_gate.q, "shared_expert_gate", 1, 1, D));
     }
     return Ok();
+}
+
+namespace models {
+static Status check_block_f32(const mrun_sparse_moe *m);  // float32 blocks, below
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -647,7 +655,11 @@ const char *mrun_last_error(void) { return g_last_error.c_str(); }
 
 const char *mrun_version(void) { return "mrun-moe 0.1.0 (gfx950)"; }
 
-int mrun_moe_check(const mrun_sparse_moe *moe) { return report(check_block(moe)); }
+int mrun_moe_check(const mrun_sparse_moe *moe) {
+    // a block of f32 experts is an f32 block (mrun_moe_forward_f32) and is checked as one
+    if (moe && moe->switch_gate_proj.bits == 32) return report(models::check_block_f32(moe));
+    return report(check_block(moe));
+}
 
 size_t mrun_moe_workspace_bytes(const mrun_moe_config *cfg, int32_t tokens) {
     if (!cfg || tokens <= 0 || !check_config(*cfg).ok()) return 0;
@@ -667,6 +679,159 @@ int mrun_moe_forward(const mrun_sparse_moe *moe, const mrun_bf16 *x, int32_t tok
     if (st.ok())
         st = models::sparse_moe_forward(*moe, x, tokens, out, (char *)workspace, workspace_bytes,
                                         (hipStream_t)stream);
+    return report(st);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------------------------
+// float32 blocks: SparseMoe::forward (moe.rs:149-174) with every tensor f32, as the reference runs
+// an f32 checkpoint (its dense gather_mm, nuvec.rs:688-697, and every other op then compute and
+// keep f32). The weights are dense f32 stacked weights (bits 32); the op sequence is the bf16
+// forward's without its bf16 roundings.
+
+namespace mrun {
+namespace models {
+
+static Status check_f32(const mrun_quantized &q, const std::string &path, int experts, int out,
+                        int in) {
+    if (q.bits != 32 || !q.weight)
+        return Err(MRUN_ERR_INVALID, path + ": an f32 block takes dense f32 weights (bits 32)");
+    if (q.scales || q.biases)
+        return Err(MRUN_ERR_INVALID, path + ": dense f32 weights carry no scales or biases");
+    if (q.experts != experts || q.out != out || q.in != in)
+        return Err(MRUN_ERR_INVALID, path + ": shape [" + std::to_string(q.experts) + ", " +
+                                         std::to_string(q.out) + ", " + std::to_string(q.in) +
+                                         "], expected [" + std::to_string(experts) + ", " +
+                                         std::to_string(out) + ", " + std::to_string(in) + "]");
+    return check_ptr(q.weight, path.c_str());
+}
+
+static Status check_f32_linear(const mrun_linear &l, const std::string &path, int out, int in) {
+    if (l.weight)
+        return Err(MRUN_ERR_INVALID,
+                   path + ": an f32 block's Linear carries its weight in q (bits 32)");
+    if (l.bias) return Err(MRUN_ERR_UNSUPPORTED, path + ": f32 Linear biases are not run");
+    return check_f32(l.q, path, 1, out, in);
+}
+
+static Status check_block_f32(const mrun_sparse_moe *m) {
+    if (!m) return Err(MRUN_ERR_INVALID, "moe is null");
+    const mrun_moe_config &c = m->cfg;
+    TRY(check_config(c));
+    const int D = c.hidden, E = c.experts, I = c.intermediate, S = c.shared_intermediate;
+    TRY(check_f32_linear(m->gate, "gate", E, D));
+    TRY(check_f32(m->switch_gate_proj, "switch_mlp.gate_proj", E, I, D));
+    TRY(check_f32(m->switch_up_proj, "switch_mlp.up_proj", E, I, D));
+    TRY(check_f32(m->switch_down_proj, "switch_mlp.down_proj", E, D, I));
+    if (S > 0) {
+        TRY(check_f32_linear(m->shared_gate_proj, "shared_expert.gate_proj", S, D));
+        TRY(check_f32_linear(m->shared_up_proj, "shared_expert.up_proj", S, D));
+        TRY(check_f32_linear(m->shared_down_proj, "shared_expert.down_proj", D, S));
+        TRY(check_f32_linear(m->shared_expert_gate, "shared_expert_gate", 1, D));
+    }
+    return Ok();
+}
+
+// logits [T, E], ids [T, k], scores [T, k], act [P, I], y [P, D]; with a shared expert its gate
+// logit [T], act [T, S] and output [T, D] (all f32 but the ids)
+struct PlanF32 {
+    size_t logits, ids, scores, act, y, sh_logit, sh_act, sh_y, total;
+};
+
+static PlanF32 plan_f32(const mrun_moe_config &c, int T) {
+    PlanF32 p{};
+    size_t at = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = at;
+        at += a256(bytes);
+        return o;
+    };
+    const size_t P = (size_t)T * c.top_k, S = (size_t)c.shared_intermediate;
+    p.logits = take(4 * (size_t)T * c.experts);
+    p.ids = take(4 * P);
+    p.scores = take(4 * P);
+    p.act = take(4 * P * c.intermediate);
+    p.y = take(4 * P * c.hidden);
+    if (S) {
+        p.sh_logit = take(4 * (size_t)T);
+        p.sh_act = take(4 * (size_t)T * S);
+        p.sh_y = take(4 * (size_t)T * c.hidden);
+    }
+    p.total = at;
+    return p;
+}
+
+static Status sparse_moe_forward_f32(const mrun_sparse_moe &m, const float *x, int T, float *out,
+                                     char *ws, size_t ws_bytes, hipStream_t s) {
+    const mrun_moe_config &c = m.cfg;
+    const PlanF32 p = plan_f32(c, T);
+    if (ws_bytes < p.total)
+        return Err(MRUN_ERR_WORKSPACE, "workspace of " + std::to_string(ws_bytes) +
+                                           " bytes, need " + std::to_string(p.total));
+    const int D = c.hidden, E = c.experts, k = c.top_k, I = c.intermediate,
+              S = c.shared_intermediate, P = T * k;
+    float *logits = (float *)(ws + p.logits), *scores = (float *)(ws + p.scores);
+    uint32_t *ids = (uint32_t *)(ws + p.ids);
+    float *act = (float *)(ws + p.act), *y = (float *)(ws + p.y);
+    auto W = [](const mrun_quantized &q) { return (const float *)q.weight; };
+    // router: gates = softmax(gate(x)), top-k, scores (moe.rs:151-159)
+    TRY_HIP(launch_f32_rows(F32Rows{x, 1, D, W(m.gate.q), nullptr, nullptr, T, E, logits}, false, s),
+            "f32 router");
+    TRY_HIP(launch_f32_topk(logits, T, E, k, c.norm_topk_prob != 0, ids, scores, s), "f32 top-k");
+    // SwitchGlu (moe.rs:61-94): pair p = t k + j reads token t's row and expert ids[p]
+    TRY_HIP(launch_f32_rows(F32Rows{x, k, D, W(m.switch_gate_proj), W(m.switch_up_proj), ids, P, I,
+                                    act},
+                            true, s),
+            "f32 experts gate/up");
+    TRY_HIP(launch_f32_rows(F32Rows{act, 1, I, W(m.switch_down_proj), nullptr, ids, P, D, y}, false,
+                            s),
+            "f32 experts down");
+    // the shared expert under its sigmoid gate (moe.rs:166-171)
+    const float *gl = nullptr, *sy = nullptr;
+    if (S > 0) {
+        float *sh_logit = (float *)(ws + p.sh_logit), *sh_act = (float *)(ws + p.sh_act),
+              *sh_y = (float *)(ws + p.sh_y);
+        TRY_HIP(launch_f32_rows(F32Rows{x, 1, D, W(m.shared_expert_gate.q), nullptr, nullptr, T, 1,
+                                        sh_logit},
+                                false, s),
+                "f32 shared gate");
+        TRY_HIP(launch_f32_rows(F32Rows{x, 1, D, W(m.shared_gate_proj.q), W(m.shared_up_proj.q),
+                                        nullptr, T, S, sh_act},
+                                true, s),
+                "f32 shared gate/up");
+        TRY_HIP(launch_f32_rows(F32Rows{sh_act, 1, S, W(m.shared_down_proj.q), nullptr, nullptr, T,
+                                        D, sh_y},
+                                false, s),
+                "f32 shared down");
+        gl = sh_logit, sy = sh_y;
+    }
+    TRY_HIP(launch_f32_combine(y, scores, T, k, D, gl, sy, out, s), "f32 combine");
+    return Ok();
+}
+
+}  // namespace models
+}  // namespace mrun
+
+extern "C" {
+
+size_t mrun_moe_workspace_bytes_f32(const mrun_moe_config *cfg, int32_t tokens) {
+    if (!cfg || tokens <= 0 || !check_config(*cfg).ok()) return 0;
+    return models::plan_f32(*cfg, tokens).total;
+}
+
+int mrun_moe_forward_f32(const mrun_sparse_moe *moe, const float *x, int32_t tokens, float *out,
+                         void *workspace, size_t workspace_bytes, mrun_stream_t stream) {
+    Status st = models::check_block_f32(moe);
+    if (st.ok() && tokens < 0) st = Err(MRUN_ERR_INVALID, "tokens must not be negative");
+    if (st.ok() && tokens == 0) return report(st);  // an empty batch: nothing to do
+    if (st.ok()) st = check_ptr(x, "x");
+    if (st.ok()) st = check_ptr(out, "out");
+    if (st.ok()) st = check_ptr(workspace, "workspace");
+    if (st.ok() && (const void *)x == (const void *)out) st = Err(MRUN_ERR_INVALID, "out must not alias x");
+    if (st.ok())
+        st = models::sparse_moe_forward_f32(*moe, x, tokens, out, (char *)workspace,
+                                            workspace_bytes, (hipStream_t)stream);
     return report(st);
 }
 

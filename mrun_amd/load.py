@@ -14,7 +14,7 @@ from pathlib import Path
 
 from . import _lib
 from ._lib import MoeConfig, SparseMoe as _SparseMoe, check
-from .moe import SparseMoe
+from .moe import SparseMoe, SparseMoeF32
 
 
 class Weights:
@@ -68,6 +68,8 @@ class Weights:
         view = _SparseMoe()
         check(self._lib.mrun_weights_load_moe(self._h, prefix.encode(), ctypes.byref(cfg),
                                               ctypes.byref(view)))
+        if view.switch_gate_proj.bits == 32:  # an f32 checkpoint's block
+            return SparseMoeF32.from_view(view, owner=self)
         return SparseMoe.from_view(view, owner=self)
 
     def load_bf16(self, name: str, n: int) -> int:

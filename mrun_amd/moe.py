@@ -220,6 +220,73 @@ class SparseMoe:
 _SYNTH_DEV = None
 
 
+class SparseMoeF32:
+    """SparseMoe (moe.rs:109-188) of a float32 checkpoint: every tensor f32 on the device, run by
+    mrun_moe_forward_f32 (each weight a dense bits-32 stacked weight)."""
+
+    def __init__(self, fb, device="cuda"):
+        """From host f32 arrays (synth.F32Block)."""
+        s = fb.shape
+        self.shape = s
+        self.device = torch.device(device)
+        f32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(device)
+        self._t = {}
+
+        def q(name, a, experts):
+            t = self._t[name] = f32(a)
+            return Quantized(_ptr(t).value, None, None, experts, a.shape[-2], a.shape[-1], 0, 32)
+
+        lin = lambda name, a: Linear(None, q(name, a, 1), None, a.shape[-2], a.shape[-1])
+        self.cfg = MoeConfig(s.hidden, s.experts, s.top_k, s.intermediate, int(s.norm_topk),
+                             s.shared)
+        m = _SparseMoe()
+        m.cfg = self.cfg
+        m.gate = lin("router", fb.router)
+        m.switch_gate_proj = q("gate_proj", fb.gate_proj, s.experts)
+        m.switch_up_proj = q("up_proj", fb.up_proj, s.experts)
+        m.switch_down_proj = q("down_proj", fb.down_proj, s.experts)
+        if s.shared:
+            m.shared_gate_proj = lin("sh_gate_proj", fb.sh_gate_proj)
+            m.shared_up_proj = lin("sh_up_proj", fb.sh_up_proj)
+            m.shared_down_proj = lin("sh_down_proj", fb.sh_down_proj)
+            m.shared_expert_gate = lin("sh_expert_gate", fb.sh_expert_gate)
+        self.c = m
+        check(_lib.load().mrun_moe_check(ctypes.byref(self.c)))
+        self._ws = None
+
+    @classmethod
+    def from_view(cls, view: "_SparseMoe", owner=None, device="cuda") -> "SparseMoeF32":
+        """An f32 block over device memory someone else owns (a loaded f32 checkpoint)."""
+        self = cls.__new__(cls)
+        c = view.cfg
+        self.shape = Shape(hidden=c.hidden, experts=c.experts, top_k=c.top_k,
+                           intermediate=c.intermediate, shared=c.shared_intermediate,
+                           norm_topk=bool(c.norm_topk_prob))
+        self.device = torch.device(device)
+        self.cfg = MoeConfig(c.hidden, c.experts, c.top_k, c.intermediate, c.norm_topk_prob,
+                             c.shared_intermediate)
+        self.c = view
+        self._owner = owner
+        self._ws = None
+        check(_lib.load().mrun_moe_check(ctypes.byref(self.c)))
+        return self
+
+    def workspace_bytes(self, tokens: int) -> int:
+        return int(_lib.load().mrun_moe_workspace_bytes_f32(ctypes.byref(self.cfg), tokens))
+
+    def forward(self, x: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+        """x [T, hidden] f32 -> [T, hidden] f32."""
+        T = x.shape[0]
+        if out is None:
+            out = torch.empty_like(x)
+        need = max(self.workspace_bytes(T), 1)
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(need, dtype=torch.uint8, device=self.device)
+        check(_lib.load().mrun_moe_forward_f32(ctypes.byref(self.c), _ptr(x), T, _ptr(out),
+                                               _ptr(self._ws), self._ws.numel(), _stream(stream)))
+        return out
+
+
 def _synth_dev() -> ctypes.CDLL:
     global _SYNTH_DEV
     if _SYNTH_DEV is None:

@@ -255,6 +255,50 @@ def make_block(shape: Shape, config: int = CFG_DECODE, layer: int = 0,
     return blk
 
 
+@dataclass
+class F32Block:
+    """The tensors of one SparseMoe of a float32 checkpoint, all dense f32 [out, in] rows: router
+    [E, D], gate/up [E, I, D], down [E, D, I]; with a shared expert its gate/up [S, D], down [D, S]
+    and gate [1, D]."""
+
+    shape: Shape
+    router: np.ndarray
+    gate_proj: np.ndarray
+    up_proj: np.ndarray
+    down_proj: np.ndarray
+    sh_gate_proj: np.ndarray | None = None
+    sh_up_proj: np.ndarray | None = None
+    sh_down_proj: np.ndarray | None = None
+    sh_expert_gate: np.ndarray | None = None
+
+
+def normal_f32(s: int, shape: tuple, std: float) -> np.ndarray:
+    """f32 N(0, std) from numpy's PCG64 seeded with s (full f32 mantissas, unlike the bf16 draws)."""
+    return (np.random.default_rng(s).standard_normal(shape) * std).astype(np.float32)
+
+
+def make_block_f32(shape: Shape, config: int = CFG_PLUMBING, layer: int = 0) -> F32Block:
+    """A seeded f32 block: weights N(0, 1/sqrt(in)), the router N(0, 2/sqrt(D)) so that its
+    softmax is far from uniform."""
+    D, E, I, S = shape.hidden, shape.experts, shape.intermediate, shape.shared
+    w = lambda tid, shp: normal_f32(seed(config, layer, tid), shp, 1.0 / np.sqrt(shp[-1]))
+    blk = F32Block(shape=shape,
+                   router=normal_f32(seed(config, layer, ROUTER_W), (E, D), 2.0 / np.sqrt(D)),
+                   gate_proj=w(GATE_CODES, (E, I, D)), up_proj=w(UP_CODES, (E, I, D)),
+                   down_proj=w(DOWN_CODES, (E, D, I)))
+    if S:
+        blk.sh_gate_proj = w(SH_GATE_CODES, (S, D))
+        blk.sh_up_proj = w(SH_UP_CODES, (S, D))
+        blk.sh_down_proj = w(SH_DOWN_CODES, (D, S))
+        blk.sh_expert_gate = w(SH_EXPERT_GATE, (1, D))
+    return blk
+
+
+def make_x_f32(shape: Shape, tokens: int, config: int = CFG_PLUMBING, layer: int = 0) -> np.ndarray:
+    """f32 N(0,1) activations [tokens, hidden]."""
+    return normal_f32(seed(config, layer, X), (tokens, shape.hidden), 1.0)
+
+
 def make_x(shape: Shape, tokens: int, config: int = CFG_DECODE, layer: int = 0) -> np.ndarray:
     """bf16 N(0,1) activations [tokens, hidden]."""
     return normal_bf16(seed(config, layer, X), tokens * shape.hidden, 1.0).reshape(

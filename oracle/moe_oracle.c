@@ -552,6 +552,94 @@ done:
     return rc;
 }
 
+/* ---- the block in f32 (an f32 checkpoint: moe.rs:149-174 with no bf16 rounding) ---- */
+
+static float dot32(const float *a, const float *w, int32_t n) {
+    float acc = 0.0f;
+    for (int32_t i = 0; i < n; i++) acc = acc + a[i] * w[i];
+    return acc;
+}
+
+int orc_moe_forward_f32(const orc_block_f32 *b, const float *x, int32_t T, float *out,
+                        uint32_t *ids_out) {
+    if (!b || !x || !out || T <= 0) return -1;
+    const orc_config *c = &b->cfg;
+    const int32_t D = c->hidden, E = c->experts, k = c->top_k, I = c->intermediate;
+    const int32_t S = c->shared_intermediate;
+    if (D <= 0 || E <= 0 || I <= 0 || k < 1 || k > E || S < 0) return -1;
+    if (!b->router || !b->sw_gate || !b->sw_up || !b->sw_down) return -1;
+    if (S > 0 && (!b->sh_gate || !b->sh_up || !b->sh_down || !b->sh_expert_gate)) return -1;
+    int rc = 0;
+#pragma omp parallel for schedule(dynamic)
+    for (int32_t t = 0; t < T; t++) {
+        const float *xt = x + (size_t)t * D;
+        float *gates = malloc(sizeof(float) * (size_t)E);
+        int *taken = calloc((size_t)E, sizeof(int));
+        float *act = malloc(sizeof(float) * (size_t)(I > S ? I : S));
+        float *acc = malloc(sizeof(float) * (size_t)D);
+        uint32_t ids[64];
+        float sc[64];
+        if (!gates || !taken || !act || !acc || k > 64) {
+#pragma omp atomic write
+            rc = -1;
+            free(gates), free(taken), free(act), free(acc);
+            continue;
+        }
+        /* router: softmax(x W^T) over the experts (moe.rs:151-155) */
+        float m = -INFINITY, sum = 0.0f;
+        for (int32_t e = 0; e < E; e++) {
+            gates[e] = dot32(xt, b->router + (size_t)e * D, D);
+            m = gates[e] > m ? gates[e] : m;
+        }
+        for (int32_t e = 0; e < E; e++) {
+            gates[e] = expf(gates[e] - m);
+            sum = sum + gates[e];
+        }
+        for (int32_t e = 0; e < E; e++) gates[e] = gates[e] / sum;
+        /* top-k in rank order, equal gates by lower id; scores (moe.rs:156-159) */
+        float tot = 0.0f;
+        for (int32_t j = 0; j < k; j++) {
+            int32_t best = -1;
+            for (int32_t e = 0; e < E; e++)
+                if (!taken[e] && (best < 0 || gates[e] > gates[best])) best = e;
+            taken[best] = 1;
+            ids[j] = (uint32_t)best;
+            sc[j] = gates[best];
+            tot = tot + sc[j];
+        }
+        if (c->norm_topk_prob)
+            for (int32_t j = 0; j < k; j++) sc[j] = sc[j] / tot;
+        /* experts: y = down(silu(gate x) * up x); routed = sum_j y_j * score_j (moe.rs:79-94,
+           160-165) */
+        for (int32_t d = 0; d < D; d++) acc[d] = 0.0f;
+        for (int32_t j = 0; j < k; j++) {
+            const size_t e = ids[j];
+            for (int32_t i = 0; i < I; i++) {
+                float g = dot32(xt, b->sw_gate + (e * I + i) * D, D);
+                float u = dot32(xt, b->sw_up + (e * I + i) * D, D);
+                act[i] = (g * sigmoid_f32(g)) * u;
+            }
+            for (int32_t d = 0; d < D; d++)
+                acc[d] = acc[d] + dot32(act, b->sw_down + (e * D + d) * I, I) * sc[j];
+        }
+        /* the shared expert under its sigmoid gate (moe.rs:166-171) */
+        if (S > 0) {
+            float sg = sigmoid_f32(dot32(xt, b->sh_expert_gate, D));
+            for (int32_t i = 0; i < S; i++) {
+                float g = dot32(xt, b->sh_gate + (size_t)i * D, D);
+                float u = dot32(xt, b->sh_up + (size_t)i * D, D);
+                act[i] = (g * sigmoid_f32(g)) * u;
+            }
+            for (int32_t d = 0; d < D; d++)
+                acc[d] = acc[d] + sg * dot32(act, b->sh_down + (size_t)d * S, S);
+        }
+        memcpy(out + (size_t)t * D, acc, sizeof(float) * (size_t)D);
+        if (ids_out) memcpy(ids_out + (size_t)t * k, ids, sizeof(uint32_t) * (size_t)k);
+        free(gates), free(taken), free(act), free(acc);
+    }
+    return rc;
+}
+
 int orc_moe_stack(const orc_block *blocks, int32_t n_layers, const orc_bf16 *norm_w, float eps,
                   orc_bf16 *x, int32_t T) {
     if (!blocks || n_layers <= 0 || !x || T <= 0) return -1;

@@ -40,6 +40,8 @@
  *   orc_rms_norm           torch.nn.functional.rms_norm in float32
  *   orc_moe_forward        an independent numpy float64 restatement of the whole block with the
  *                          same rounding points, on tiny and small shapes
+ *   orc_moe_forward_f32    the same numpy restatement without roundings (float64, within f32
+ *                          accumulation error); closed forms of one-expert and zero-weight blocks
  * Functions whose arithmetic only nuvec could pin (its accumulation order, its exp, its
  * argpartition tie order) are pinned by the checks above to within those freedoms.
  */
@@ -173,6 +175,25 @@ int orc_topk_valid(const orc_bf16 *gates, const orc_bf16 *logits, int32_t n, int
  * blocks: n_layers blocks; x [T, D] is updated in place. */
 int orc_moe_stack(const orc_block *blocks, int32_t n_layers, const orc_bf16 *norm_w, float eps,
                   orc_bf16 *x, int32_t T);
+
+/* A SparseMoe whose tensors are all float32 (an f32 checkpoint: the reference's Hugging Face
+ * fixture, gen_tiny.py:235-274). Dense weights, row-major: router [E, D], gate/up [E, I, D],
+ * down [E, D, I]; with shared_intermediate S > 0: shared gate/up [S, D], down [D, S] and the
+ * shared expert's gate [D]. */
+typedef struct {
+    orc_config cfg;
+    const float *router, *sw_gate, *sw_up, *sw_down;
+    const float *sh_gate, *sh_up, *sh_down, *sh_expert_gate;
+} orc_block_f32;
+
+/* SparseMoe::forward (moe.rs:149-174) of an f32 block on x [T, D] -> out [T, D]: the op sequence
+ * of orc_moe_forward with every tensor kept in f32 (no bf16 rounding). Contractions accumulate in
+ * f32 in ascending index order; softmax max, exp(l - max), sum in ascending expert order; top-k
+ * with equal gates ranked by the lower id; scores = gates, or gates / (their sum in rank order);
+ * routed = sum over the token's pairs in rank order of y * score; out = routed +
+ * sigmoid(gate logit) * shared. ids_out [T, k] optional. Returns 0, or -1 on invalid arguments. */
+int orc_moe_forward_f32(const orc_block_f32 *b, const float *x, int32_t T, float *out,
+                        uint32_t *ids_out);
 
 /* Threads the oracle's parallel loops use (OpenMP); 0 = leave the default. Returns the count. */
 int orc_set_threads(int32_t n);

@@ -38,6 +38,11 @@ class OrcBlock(ctypes.Structure):
                 ("sh_down", OrcLinear), ("sh_expert_gate", OrcLinear)]
 
 
+class OrcBlockF32(ctypes.Structure):
+    _fields_ = [("cfg", OrcConfig)] + [(n, c_void_p) for n in (
+        "router", "sw_gate", "sw_up", "sw_down", "sh_gate", "sh_up", "sh_down", "sh_expert_gate")]
+
+
 class OrcTrace(ctypes.Structure):
     _fields_ = [(n, c_void_p) for n in ("logits", "gates", "ids", "scores", "order", "inverse",
                                         "act", "y", "routed", "shared_gate", "shared_y")]
@@ -79,7 +84,9 @@ def lib() -> ctypes.CDLL:
         l.orc_moe_stack.argtypes = [POINTER(OrcBlock), c_int32, c_void_p, c_float, c_void_p,
                                     c_int32]
         l.orc_set_threads.argtypes = [c_int32]
-        for name in ("orc_linear_forward", "orc_qmatmul", "orc_gather_qmm", "orc_topk",
+        l.orc_moe_forward_f32.argtypes = [POINTER(OrcBlockF32), c_void_p, c_int32, c_void_p,
+                                          c_void_p]
+        for name in ("orc_moe_forward_f32", "orc_linear_forward", "orc_qmatmul", "orc_gather_qmm", "orc_topk",
                      "orc_permute", "orc_moe_forward", "orc_topk_valid", "orc_moe_stack",
                      "orc_set_threads"):
             getattr(l, name).restype = c_int32
@@ -180,6 +187,29 @@ def moe_forward(hb, x: np.ndarray, forced_ids: np.ndarray | None = None, trace: 
     if rc != 0:
         raise RuntimeError(f"orc_moe_forward failed ({rc})")
     return (out, t) if trace else out
+
+
+def moe_forward_f32(fb, x: np.ndarray):
+    """SparseMoe::forward of an f32 block (duck-typed synth.F32Block) on the CPU: (out [T, D]
+    float32, ids [T, k])."""
+    keep = _Keep()
+    s = fb.shape
+    b = OrcBlockF32()
+    b.cfg = OrcConfig(s.hidden, s.experts, s.top_k, s.intermediate, int(s.norm_topk), s.shared)
+    names = ["router", "sw_gate", "sw_up", "sw_down"] + (
+        ["sh_gate", "sh_up", "sh_down", "sh_expert_gate"] if s.shared else [])
+    src = {"router": fb.router, "sw_gate": fb.gate_proj, "sw_up": fb.up_proj,
+           "sw_down": fb.down_proj, "sh_gate": fb.sh_gate_proj, "sh_up": fb.sh_up_proj,
+           "sh_down": fb.sh_down_proj, "sh_expert_gate": fb.sh_expert_gate}
+    for n in names:
+        setattr(b, n, _p(keep(src[n], np.float32)))
+    x = keep(x, np.float32)
+    T = x.shape[0]
+    out = np.empty((T, s.hidden), np.float32)
+    ids = np.empty((T, s.top_k), np.uint32)
+    if lib().orc_moe_forward_f32(ctypes.byref(b), _p(x), T, _p(out), _p(ids)) != 0:
+        raise RuntimeError("orc_moe_forward_f32 failed")
+    return out, ids
 
 
 def moe_stack(blocks, x: np.ndarray, norm_w: np.ndarray | None = None, eps: float = 1e-6):

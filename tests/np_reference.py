@@ -95,3 +95,31 @@ def forward(hb, x_bits: np.ndarray, ids: np.ndarray | None = None):
         "logits": f32_to_bf16(logits.astype(np.float32)), "gates": gates_bits, "ids": ids,
         "scores": f32_to_bf16(sc.astype(np.float32)),
     }
+
+
+def forward_f32(fb, x: np.ndarray):
+    """SparseMoe::forward of an f32 block (synth.F32Block) in float64 with no rounding at all:
+    (out [T, D], gates [T, E], ids [T, k]); ids by a brute-force lexsort (gate desc, id asc)."""
+    s = fb.shape
+    x = np.asarray(x, np.float64)
+    T, k = x.shape[0], s.top_k
+    logits = x @ np.asarray(fb.router, np.float64).T
+    e = np.exp(logits - logits.max(axis=1, keepdims=True))
+    gates = e / e.sum(axis=1, keepdims=True)
+    ids = np.stack([np.lexsort((np.arange(s.experts), -gates[t]))[:k] for t in range(T)])
+    sc = np.take_along_axis(gates, ids, axis=1)
+    if s.norm_topk:
+        sc = sc / sc.sum(axis=1, keepdims=True)
+    Wg, Wu, Wd = (np.asarray(a, np.float64) for a in (fb.gate_proj, fb.up_proj, fb.down_proj))
+    out = np.zeros((T, s.hidden))
+    for t in range(T):
+        for j in range(k):
+            ex = int(ids[t, j])
+            g, u = Wg[ex] @ x[t], Wu[ex] @ x[t]
+            out[t] += (Wd[ex] @ (g * sigmoid(g) * u)) * sc[t, j]
+    if s.shared:
+        sg = sigmoid(x @ np.asarray(fb.sh_expert_gate, np.float64).reshape(-1))
+        g = x @ np.asarray(fb.sh_gate_proj, np.float64).T
+        u = x @ np.asarray(fb.sh_up_proj, np.float64).T
+        out += sg[:, None] * ((g * sigmoid(g) * u) @ np.asarray(fb.sh_down_proj, np.float64).T)
+    return out, gates, ids.astype(np.uint32)

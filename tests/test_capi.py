@@ -128,6 +128,63 @@ def test_invalid_blocks_are_refused(over, code, text):
     assert rc == code and text in msg, (rc, msg)
 
 
+def f32_block(D=256, E=64, k=8, I=128, S=128, **over):
+    """A block of dense f32 weights (bits 32), as mrun_moe_forward_f32 takes it."""
+    d = lambda e, o, i: Quantized(FAKE, None, None, e, o, i, 0, 32)
+    lin = lambda o, i: Linear(None, d(1, o, i), None, o, i)
+    m = SparseMoe()
+    m.cfg = MoeConfig(D, E, k, I, 1, S)
+    m.gate = lin(E, D)
+    m.switch_gate_proj, m.switch_up_proj, m.switch_down_proj = d(E, I, D), d(E, I, D), d(E, D, I)
+    if S:
+        m.shared_gate_proj, m.shared_up_proj = lin(S, D), lin(S, D)
+        m.shared_down_proj, m.shared_expert_gate = lin(D, S), lin(1, D)
+    for k_, v in over.items():
+        setattr(m, k_, v)
+    return m
+
+
+def test_f32_blocks():
+    """f32 blocks (bits 32 everywhere) pass the check; a bf16 or quantized weight among them, a
+    Linear bias or scales are refused; the bf16 forward refuses them before any device work, and
+    the f32 forward's workspace is sized from the config alone."""
+    lib = _lib.load()
+    assert status(f32_block()) == (0, "")
+    assert status(f32_block(S=0)) == (0, "")
+    d = lambda e, o, i: Quantized(FAKE, None, None, e, o, i, 0, 32)
+    cases = [
+        ({"gate": Linear(FAKE, Quantized(), None, 64, 256)}, _lib.MRUN_ERR_INVALID,
+         "gate: an f32 block's Linear carries its weight in q"),
+        ({"shared_up_proj": Linear(None, q(1, 128, 256), None, 128, 256)}, _lib.MRUN_ERR_INVALID,
+         "shared_expert.up_proj: an f32 block takes dense f32 weights"),
+        ({"switch_down_proj": Quantized(FAKE, FAKE, None, 64, 256, 128, 0, 32)},
+         _lib.MRUN_ERR_INVALID, "carry no scales"),
+        ({"switch_up_proj": d(64, 128, 255)}, _lib.MRUN_ERR_INVALID, "switch_mlp.up_proj: shape"),
+        ({"shared_expert_gate": Linear(None, d(1, 1, 256), FAKE, 1, 256)},
+         _lib.MRUN_ERR_UNSUPPORTED, "f32 Linear biases"),
+    ]
+    for over, code, text in cases:
+        rc, msg = status(f32_block(**over))
+        assert rc == code and text in msg, (over, rc, msg)
+    m = f32_block()
+    rc = lib.mrun_moe_forward(ctypes.byref(m), FAKE, 4, FAKE * 2, FAKE * 3, 1 << 30, None)
+    msg = lib.mrun_last_error().decode()
+    assert rc == _lib.MRUN_ERR_UNSUPPORTED and "run through mrun_moe_forward_f32" in msg, msg
+    # a bf16 block is not an f32 one
+    rc = lib.mrun_moe_forward_f32(ctypes.byref(block()), FAKE, 4, FAKE * 2, FAKE * 3, 1 << 30, None)
+    assert rc == _lib.MRUN_ERR_INVALID, lib.mrun_last_error()
+    cfg = MoeConfig(256, 64, 8, 128, 1, 128)
+    T, P = 5, 40
+    a = lambda n: (n + 255) // 256 * 256
+    want = a(4 * T * 64) + 2 * a(4 * P) + a(4 * P * 128) + a(4 * P * 256) + a(4 * T) \
+        + a(4 * T * 128) + a(4 * T * 256)
+    assert lib.mrun_moe_workspace_bytes_f32(ctypes.byref(cfg), T) == want
+    assert lib.mrun_moe_workspace_bytes_f32(ctypes.byref(cfg), 0) == 0
+    rc = lib.mrun_moe_forward_f32(ctypes.byref(m), FAKE, 4, FAKE * 2, FAKE * 3, 64, None)
+    assert rc == _lib.MRUN_ERR_WORKSPACE, lib.mrun_last_error()
+    assert lib.mrun_moe_forward_f32(ctypes.byref(m), FAKE, 0, None, None, 0, None) == 0
+
+
 def test_top_k_must_fit_the_experts():
     m = block()
     m.cfg = MoeConfig(2048, 256, 257, 512, 1, 512)

@@ -290,6 +290,58 @@ def test_block_8bit_and_quantized_gates_match_numpy(shape, T, expert_bits, gate_
     assert s["max_abs"] < 2e-3, s
 
 
+# ---- the f32 block (an f32 checkpoint: every op in f32, no bf16 rounding) -------------------
+
+F32_TOL = 2e-6  # of the largest |output|: f32 accumulation over at most a few thousand terms
+
+
+@pytest.mark.parametrize("shape,T", [
+    (synth.Shape(hidden=64, experts=8, top_k=2, intermediate=32, shared=32), 7),
+    (synth.Shape(hidden=64, experts=8, top_k=8, intermediate=32, shared=0, norm_topk=False), 5),
+    (synth.Shape(hidden=256, experts=64, top_k=8, intermediate=128, shared=128), 12),
+])
+def test_block_f32_matches_float64_restatement(shape, T):
+    """orc_moe_forward_f32 against tests/np_reference.forward_f32 (float64, no rounding): the
+    same expert choice and outputs within f32 accumulation error."""
+    fb = synth.make_block_f32(shape, config=21)
+    x = synth.make_x_f32(shape, T, config=21)
+    out, ids = O.moe_forward_f32(fb, x)
+    ref, gates, rids = NP.forward_f32(fb, x)
+    assert np.array_equal(ids, rids)
+    assert np.max(np.abs(out - ref)) <= F32_TOL * np.max(np.abs(ref)), np.max(np.abs(out - ref))
+
+
+def test_block_f32_closed_forms():
+    """What the mathematics fixes without a restatement. A zero router gives every expert the
+    same gate 1/E: the top-k is then experts 0..k-1 (equal gates by lower id), scores 1/E (1/k
+    with norm). Zero down weights leave only the shared expert: sigmoid(g . x) * shared. A zero
+    shared gate weighs the shared expert by sigmoid(0) = 1/2 exactly."""
+    sh = synth.Shape(hidden=64, experts=8, top_k=3, intermediate=32, shared=32)
+    x = synth.make_x_f32(sh, 4, config=22)
+    for norm in (False, True):
+        s = synth.Shape(hidden=64, experts=8, top_k=3, intermediate=32, shared=0, norm_topk=norm)
+        fb = synth.make_block_f32(s, config=22)
+        fb.router = np.zeros_like(fb.router)
+        out, ids = O.moe_forward_f32(fb, x)
+        assert np.array_equal(ids, np.tile(np.arange(3, dtype=np.uint32), (4, 1)))
+        w = 1.0 / 3 if norm else 1.0 / 8
+        X = x.astype(np.float64)
+        want = np.zeros((4, 64))
+        for e in range(3):
+            g = X @ fb.gate_proj[e].T.astype(np.float64)
+            u = X @ fb.up_proj[e].T.astype(np.float64)
+            want += ((g / (1 + np.exp(-g)) * u) @ fb.down_proj[e].T.astype(np.float64)) * w
+        assert np.max(np.abs(out - want)) <= F32_TOL * np.max(np.abs(want))
+    fb = synth.make_block_f32(sh, config=22)
+    fb.down_proj = np.zeros_like(fb.down_proj)
+    fb.sh_expert_gate = np.zeros_like(fb.sh_expert_gate)
+    out, _ = O.moe_forward_f32(fb, x)
+    X = x.astype(np.float64)
+    g, u = X @ fb.sh_gate_proj.T.astype(np.float64), X @ fb.sh_up_proj.T.astype(np.float64)
+    want = 0.5 * ((g / (1 + np.exp(-g)) * u) @ fb.sh_down_proj.T.astype(np.float64))
+    assert np.max(np.abs(out - want)) <= F32_TOL * np.max(np.abs(want))
+
+
 def test_quantize_round_trip():
     """synth.quantize: every weight within half a step of its dequantised value."""
     w = synth.normal_bf16(synth.seed(1, 0, synth.ROUTER_W), 16 * 256, 0.02).reshape(16, 256)
