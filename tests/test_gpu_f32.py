@@ -51,6 +51,21 @@ def test_f32_block_matches_oracle(shape, Ts):
         check(fb, dev, synth.make_x_f32(shape, T, config=23, layer=T), f"{shape.name} T={T}")
 
 
+@pytest.mark.parametrize("shape,T", [
+    # 512 experts (eight keys per lane in the top-k) and k = 16, the largest the build takes
+    (synth.Shape(hidden=128, experts=512, top_k=16, intermediate=64, shared=64), 5),
+    # k = 1: scores are the gates themselves, or 1 with norm
+    (synth.Shape(hidden=128, experts=16, top_k=1, intermediate=64, shared=0), 9),
+    (synth.Shape(hidden=128, experts=16, top_k=1, intermediate=64, shared=0, norm_topk=False), 9),
+    # more pairs than one grid dimension holds (T k > 65535): the rows kernel strides over them
+    (synth.Shape(hidden=64, experts=8, top_k=8, intermediate=32, shared=32), 8300),
+])
+def test_f32_config_edges(shape, T):
+    fb = synth.make_block_f32(shape, config=26)
+    check(fb, M.SparseMoeF32(fb), synth.make_x_f32(shape, T, config=26, layer=T),
+          f"{shape.name} T={T}")
+
+
 def test_f32_rows_keep_their_bits():
     """A token's output does not depend on the batch around it (every dot product has a fixed
     order): rows of a 33-token batch equal the same rows run alone, bit for bit."""
