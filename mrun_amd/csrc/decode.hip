@@ -951,10 +951,12 @@ hipError_t launch_decode(const DecodeJob &j, hipStream_t s, StageMarks *marks) {
     if (marks) marks->mark(s);
 
     const int n_ch = j.D >> 5;
-    // rows per wave: 2 at T = 1 and 2 (512 and 1024 routed waves-of-rows over 8 and 16 expert
-    // slots; at T = 1 one row measured 18.9 us per block, two 18.3, four 19.5), 4 above; rows
-    // wider than 2048 take one row per wave and the streaming loop at every T
-    const int rg = n_ch > 64 ? 1 : (j.T <= 2 ? 2 : 4);
+    // rows per wave: 2 at T = 2 (1024 routed waves-of-rows over 16 expert slots), 4 otherwise; at
+    // T = 1 four rows (256 routed workgroups instead of 512, so that with the shared expert's the
+    // grid takes about one workgroup per CU) took the launch from 6.0 to 5.5 us (timed from
+    // inside) at the same bits; rows wider than 2048 take one row per wave and the streaming loop
+    // at every T
+    const int rg = n_ch > 64 ? 1 : (j.T == 2 ? 2 : 4);
     // 4 waves per workgroup: 8 and 16 (fewer redundant top-ks per CU) measured slower
     const bool b8 = j.wg.bits == 8;
     if (b8 && rg == 2) launch_k2<2, 4, 8>(j, n_ch, s);
