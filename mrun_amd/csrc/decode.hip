@@ -29,6 +29,52 @@ namespace mrun {
 
 constexpr int kMaxT = 16, kMaxP = 128;
 
+// Lane l + d's value of v for d = 16 and 32 (permlane swaps of v with itself) and l ^ 8, l ^ 4,
+// l ^ 2, l ^ 1 (DPP), each added to v: a butterfly level on lane bit 5, 4, 3, 2, 1 or 0.
+__device__ __forceinline__ float swap_add32(float a, float b) {  // lanes < 32: a; >= 32: b
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false,
+                                                    false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+__device__ __forceinline__ float swap_add16(float a, float b) {  // even rows: a; odd rows: b
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false,
+                                                    false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+__device__ __forceinline__ float butterfly_low4(float v) {  // lane bits 3, 2, 1, 0
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+    int m = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x104, 0xF, 0x5, false);  // l + 4
+    m = __builtin_amdgcn_update_dpp(m, __float_as_int(v), 0x114, 0xF, 0xA, false);      // l - 4
+    v += __int_as_float(m);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+
+// Sums over the wave of RG (2 or 4) rows' gate values g and up values u, scattered: the lanes of
+// row r's range [64 r / RG, 64 (r + 1) / RG) end with its two sums in gs and us. Whatever RG, a
+// sum pairs lanes by bit 5 of their index first, then bits 4, 3, 2, 1 and 0, so a row's sums
+// have the same bits for every RG.
+template <int RG>
+__device__ __forceinline__ void rows_reduce_scatter(const float (&g)[RG], const float (&u)[RG],
+                                                    float &gs, float &us) {
+    static_assert(RG == 2 || RG == 4, "two or four rows");
+    float g16, u16;
+    if constexpr (RG == 4) {
+        // bit 5: rows 0, 1 stay in lanes < 32, rows 2, 3 in lanes >= 32; bit 4: rows 0, 2 in the
+        // even 16-lane rows, 1, 3 in the odd ones
+        const float g32a = swap_add32(g[0], g[2]), g32b = swap_add32(g[1], g[3]);
+        const float u32a = swap_add32(u[0], u[2]), u32b = swap_add32(u[1], u[3]);
+        g16 = swap_add16(g32a, g32b);
+        u16 = swap_add16(u32a, u32b);
+    } else {
+        const float g32 = swap_add32(g[0], g[1]), u32 = swap_add32(u[0], u[1]);
+        g16 = swap_add16(g32, g32);  // bit 4 of one row: every lane adds lane l ^ 16's value
+        u16 = swap_add16(u32, u32);
+    }
+    gs = butterfly_low4(g16);
+    us = butterfly_low4(u16);
+}
+
 // Rows [row_base + g*RPI + rsub] of w0 (and w1 with glu), g < RG, for the pairs set in pm0|pm1
 // (bit p: pair p reads A row p / a_div and writes output row p). The next pair's activations are
 // loaded while the current pair is computed.
@@ -75,22 +121,18 @@ __device__ __forceinline__ void gemv_wave(const QW &w0, const QW &w1, int e, int
             if (GLU) opaque_row(r1[g]);
         }
         if constexpr (GLU && LPR == 64 && RG > 1) {
-            // every lane holds each row's sums; lane g finishes row g, so the wave evaluates the
-            // SwiGLU once for its RG rows
+            // the wave's RG gate and up sums by a reduce-scatter: row u's two sums end in lanes
+            // [64 u / RG, 64 (u + 1) / RG), and one lane of them evaluates its SwiGLU
             float s0[RG], s1[RG];
 #pragma unroll
             for (int g = 0; g < RG; ++g) {
-                s0[g] = group_sum<64>(row_part<CPL, FULL>(r0[g], xc));
-                s1[g] = group_sum<64>(row_part<CPL, FULL>(r1[g], xc));
+                s0[g] = row_part<CPL, FULL>(r0[g], xc);
+                s1[g] = row_part<CPL, FULL>(r1[g], xc);
             }
-            float a0 = s0[0], a1 = s1[0];
-#pragma unroll
-            for (int g = 1; g < RG; ++g) {
-                a0 = lane == g ? s0[g] : a0;
-                a1 = lane == g ? s1[g] : a1;
-            }
-            const int row = row_base + lane;
-            if (lane < RG && row < w0.out) {
+            float a0, a1;
+            rows_reduce_scatter<RG>(s0, s1, a0, a1);
+            const int u = lane / (64 / RG), row = row_base + u;
+            if (lane % (64 / RG) == 0 && row < w0.out) {
                 const float gt = rbf(a0), up = rbf(a1);
                 out[(size_t)p * ldo + paired_index_b<B>(row)] = (bf16_t)f2bf((gt * sigmoidf_(gt)) * up);
             }
