@@ -793,7 +793,7 @@ def main(argv=None) -> int:
         del d8, h8
 
     # between the decode sizes and the prefill chunk: block time by batch size on the configs[1]
-    # block (unbiased router); up to 32 tokens the decode schedule runs in chunks of 16
+    # block (unbiased router); the decode kernels take up to 32 tokens (256 pairs)
     batches = None
     if not args.no_sweep:
         print("[bench] batch sizes 17 to 1024", file=sys.stderr, flush=True)
@@ -803,7 +803,7 @@ def main(argv=None) -> int:
             wall, dev_ms, _ = time_forward(dev, xb, 50, 10, torch)
             batches.append({"tokens": T, "device_ms": dev_ms, "ms_per_step": wall,
                             "tokens_per_s": T / (wall * 1e-3),
-                            "schedule": "decode, chunks of 16" if T <= 32 else "prefill"})
+                            "schedule": "decode" if T <= 32 else "prefill"})
             del xb
 
     prefill = None if args.no_prefill else prefill_point(args, Q, M, synth, torch)

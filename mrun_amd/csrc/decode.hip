@@ -27,7 +27,28 @@
 
 namespace mrun {
 
-constexpr int kMaxT = 16, kMaxP = 128;
+constexpr int kMaxT = 32, kMaxP = 256;
+
+// A set of pair indices below kMaxP = 256 (one bit each), taken in ascending order. Four named
+// words rather than an array, so that the set stays in scalar registers (an indexed array went
+// to scratch memory).
+struct PairSet {
+    uint64_t m0, m1, m2, m3;
+    // the lowest pair left, removed from the set; -1 when the set is empty
+    __device__ __forceinline__ int next() {
+        if (m0) return take(m0, 0);
+        if (m1) return take(m1, 64);
+        if (m2) return take(m2, 128);
+        if (m3) return take(m3, 192);
+        return -1;
+    }
+    __device__ __forceinline__ static int take(uint64_t &w, int base) {
+        const int p = base + __ffsll((unsigned long long)w) - 1;
+        w &= w - 1;
+        return p;
+    }
+};
+static_assert(kMaxP == 256, "PairSet holds 256 pairs");
 
 // Lane l + d's value of v for d = 16 and 32 (permlane swaps of v with itself) and l ^ 8, l ^ 4,
 // l ^ 2, l ^ 1 (DPP), each added to v: a butterfly level on lane bit 5, 4, 3, 2, 1 or 0.
@@ -75,14 +96,14 @@ __device__ __forceinline__ void rows_reduce_scatter(const float (&g)[RG], const 
     us = butterfly_low4(u16);
 }
 
-// Rows [row_base + g*RPI + rsub] of w0 (and w1 with glu), g < RG, for the pairs set in pm0|pm1
-// (bit p: pair p reads A row p / a_div and writes output row p). The next pair's activations are
-// loaded while the current pair is computed.
+// Rows [row_base + g*RPI + rsub] of w0 (and w1 with glu), g < RG, for the pairs in ps (pair p
+// reads A row p / a_div and writes output row p). The next pair's activations are loaded while
+// the current pair is computed.
 // FULL: every row of the wave and every chunk of its lanes is in range (no masking).
 template <int LPR, int CPL, int RG, bool GLU, bool FULL = false, int B = 4>
 __device__ __forceinline__ void gemv_wave(const QW &w0, const QW &w1, int e, int row_base,
-                                          const bf16_t *A, int lda, int a_div, uint64_t pm0,
-                                          uint64_t pm1, bf16_t *out, int ldo, int lane) {
+                                          const bf16_t *A, int lda, int a_div, PairSet ps,
+                                          bf16_t *out, int ldo, int lane) {
     constexpr int RPI = 64 / LPR;
     const int li = lane % LPR, rsub = lane / LPR;
     const int n_ch = w0.in >> 5;
@@ -93,25 +114,12 @@ __device__ __forceinline__ void gemv_wave(const QW &w0, const QW &w1, int e, int
         load_wrow<CPL, B>(w0, e, row, li, LPR, r0[g]);
         if (GLU) load_wrow<CPL, B>(w1, e, row, li, LPR, r1[g]);
     }
-    auto next = [&](uint64_t &m0, uint64_t &m1) -> int {
-        if (m0) {
-            const int p = __ffsll((unsigned long long)m0) - 1;
-            m0 &= m0 - 1;
-            return p;
-        }
-        if (m1) {
-            const int p = 64 + __ffsll((unsigned long long)m1) - 1;
-            m1 &= m1 - 1;
-            return p;
-        }
-        return -1;
-    };
-    int p = next(pm0, pm1);
+    int p = ps.next();
     if (p < 0) return;
     XRaw cur[CPL], nxt[CPL];
     load_xrow_raw<CPL>(A + (size_t)(p / a_div) * lda, li, LPR, n_ch, cur);
     while (p >= 0) {
-        const int pn = next(pm0, pm1);
+        const int pn = ps.next();
         load_xrow_raw<CPL>(A + (size_t)((pn >= 0 ? pn : p) / a_div) * lda, li, LPR, n_ch, nxt);
         XChunk xc[CPL];
         pair_xrow<CPL, B>(cur, xc);
@@ -384,10 +392,11 @@ __device__ __forceinline__ void qrouter_row(const bf16_t *x, int T, int D, const
 // K1: router logits + the shared expert's gate logit
 
 // QUANT: some rows are quantized (a separate instantiation, so the dense-router kernel keeps its
-// registers and schedule). Four rows per workgroup, one per wave; TSPLIT (T > 2, no fused norm):
+// registers and schedule). Four rows per workgroup, one per wave; TSPLIT waves (T > 2, no fused
+// norm; 4 up to 16 tokens, 8 up to 32):
 // one row per workgroup, and wave w takes tokens [4w, 4w + 4) of it.
-template <int MAXT, bool NORM, bool QUANT, bool TSPLIT = false>
-__global__ __launch_bounds__(256) void decode_router_kernel(DecodeJob j) {
+template <int MAXT, bool NORM, bool QUANT, int TSPLIT = 0>
+__global__ __launch_bounds__(TSPLIT > 4 ? 512 : 256) void decode_router_kernel(DecodeJob j) {
     // the wave index in a scalar register: the row, its weights and the branches below are the
     // wave's own (per-lane values would make every field of a quantized row a per-lane load)
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -527,11 +536,17 @@ __device__ __forceinline__ int slot_expert(const uint32_t *mask, int nw, int slo
     return ((word >> bit) & 1u) ? w * 32 + bit : -1;
 }
 
-// Pairs choosing expert e, as a 128-bit set (one wave, from LDS).
-__device__ __forceinline__ void pairs_of(const uint32_t *sid, int P, int e, int lane,
-                                         uint64_t &pm0, uint64_t &pm1) {
-    pm0 = __ballot(lane < P && (int)sid[lane] == e);
-    pm1 = __ballot(lane + 64 < P && (int)sid[lane + 64] == e);
+// Pairs choosing expert e (one wave, from LDS).
+__device__ __forceinline__ PairSet pairs_of(const uint32_t *sid, int P, int e, int lane) {
+    PairSet ps;
+    ps.m0 = __ballot(lane < P && (int)sid[lane] == e);
+    ps.m1 = __ballot(lane + 64 < P && (int)sid[lane + 64] == e);
+    ps.m2 = ps.m3 = 0;
+    if (P > 128) {  // uniform: batches of more than 16 tokens
+        ps.m2 = __ballot(lane + 128 < P && (int)sid[lane + 128] == e);
+        ps.m3 = __ballot(lane + 192 < P && (int)sid[lane + 192] == e);
+    }
+    return ps;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -592,7 +607,7 @@ __attribute__((amdgpu_waves_per_eu(LOOP && CPL == 3 ? 3 : 1))) void decode_gateu
     if (clk && threadIdx.x == 0) atomicMin(clk, __builtin_amdgcn_s_memrealtime());
     const QW w0 = pick(j.sg, j.wg), w1 = pick(j.su, j.wu);
     int e = 0, rb, a_div, ldo;
-    uint64_t pm0, pm1;
+    PairSet ps{};
     bf16_t *out;
     if (sh) {  // shared expert gate/up: 4 * RG * RPI rows x up to 4 tokens
         const int n_row_blocks = j.S / (NW * RG * RPI * L);
@@ -600,7 +615,7 @@ __attribute__((amdgpu_waves_per_eu(LOOP && CPL == 3 ? 3 : 1))) void decode_gateu
         const int t0 = (bid / n_row_blocks) * 4;
         const int tn = min(4, j.T - t0);
         a_div = 1, ldo = j.S, out = j.sh_act;
-        pm0 = ((1ull << tn) - 1) << t0, pm1 = 0;
+        ps.m0 = ((1ull << tn) - 1) << t0;  // t0 + tn <= T <= 32
     } else {
         const int r = bid - n_sh, row_blocks = j.I / (NW * RG * RPI * L);
         const int slot = r / row_blocks;
@@ -620,11 +635,11 @@ __attribute__((amdgpu_waves_per_eu(LOOP && CPL == 3 ? 3 : 1))) void decode_gateu
         if (one) {
             if (slot >= j.k) return;
             e = __builtin_amdgcn_readfirstlane((int)sid[slot]);
-            pm0 = 1ull << slot, pm1 = 0;
+            ps.m0 = 1ull << slot;
         } else {
             e = slot_expert(mask, (j.E + 31) / 32, slot, lane);
             if (e < 0) return;
-            pairs_of(sid, j.T * j.k, e, lane, pm0, pm1);
+            ps = pairs_of(sid, j.T * j.k, e, lane);
         }
         a_div = j.k, ldo = j.I, out = j.act;
     }
@@ -632,10 +647,8 @@ __attribute__((amdgpu_waves_per_eu(LOOP && CPL == 3 ? 3 : 1))) void decode_gateu
         static_assert(!LOOP || (RG == 1 && LPR == 64), "the streaming loop takes one row per wave");
         // (two pairs' activations held at a time measured slower: 256 registers, one wave per SIMD)
         for (;;) {
-            int p;
-            if (pm0) p = __ffsll((unsigned long long)pm0) - 1, pm0 &= pm0 - 1;
-            else if (pm1) p = 64 + __ffsll((unsigned long long)pm1) - 1, pm1 &= pm1 - 1;
-            else break;
+            const int p = ps.next();
+            if (p < 0) break;
             // opaque, so nothing of one pair's pass (row addresses) is held over for the next
             int row0 = rb * L * NW + wave;
             asm volatile("" : "+v"(row0));
@@ -644,7 +657,7 @@ __attribute__((amdgpu_waves_per_eu(LOOP && CPL == 3 ? 3 : 1))) void decode_gateu
         }
     } else {
         gemv_wave<LPR, CPL, RG, true, FULL, B>(w0, w1, e, (rb * NW + wave) * RG * RPI, j.x, j.D,
-                                               a_div, pm0, pm1, out, ldo, lane);
+                                               a_div, ps, out, ldo, lane);
     }
 }
 
@@ -867,8 +880,15 @@ static void launch_k1(const DecodeJob &j, hipStream_t s) {
         // and 18.3 -> 18.6)
         dim3 g1(j.E + (j.S ? 1 : 0));
         const int nt = 64 * ((j.T + 3) / 4);
-        if (!j.router || (j.S && !j.sh_gate_w)) decode_router_kernel<4, false, true, true><<<g1, nt, 0, s>>>(j);
-        else decode_router_kernel<4, false, false, true><<<g1, nt, 0, s>>>(j);
+        const bool q = !j.router || (j.S && !j.sh_gate_w);
+        if (j.T > 16) {
+            if (q) decode_router_kernel<4, false, true, 8><<<g1, nt, 0, s>>>(j);
+            else decode_router_kernel<4, false, false, 8><<<g1, nt, 0, s>>>(j);
+        } else if (q) {
+            decode_router_kernel<4, false, true, 4><<<g1, nt, 0, s>>>(j);
+        } else {
+            decode_router_kernel<4, false, false, 4><<<g1, nt, 0, s>>>(j);
+        }
         return;
     }
     if (!j.router || (j.S && !j.sh_gate_w)) {  // a quantized router or shared gate
@@ -979,6 +999,8 @@ bool decode_supported(int D, int I, int S, int T, int k, int E) {
 }
 
 hipError_t launch_decode(const DecodeJob &j, hipStream_t s, StageMarks *marks) {
+    // the fused norm keeps the block input in the router launch's LDS: 16 tokens at most
+    if (j.norm_src && (j.T > 16 || 2 * (size_t)j.T * j.D > 65536)) return hipErrorInvalidValue;
     if (!j.router_done) {
         if (j.T == 1) launch_k1<1>(j, s);
         else if (j.T <= 4) launch_k1<4>(j, s);

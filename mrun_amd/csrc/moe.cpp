@@ -360,7 +360,8 @@ struct FusedNorm {
 // post (the layer stack): when the forward ends in the combine launch and its rows are at most
 // 2048 wide, that launch also takes the stack's residual add and next RMSNorm (post_done set, and
 // `out` is not written).
-// the largest batch that runs as decode-schedule chunks of at most 16 tokens
+// the largest batch that runs as decode-schedule chunks of at most 16 tokens, when the decode
+// kernels do not take it whole (more than 256 pairs: k above 8)
 constexpr int kChunkedDecodeMax = 32;
 
 // Workspace of a batch that runs as decode chunks: the whole batch's ids and scores where the
@@ -369,15 +370,21 @@ static size_t chunk_ws_offset(const mrun_moe_config &c, int T) {
     const Plan p = make_plan(c, T);
     return p.scores + a256(2 * (size_t)T * c.top_k);
 }
-static bool runs_chunked(int T) { return T > 16 && T <= kChunkedDecodeMax; }
-// the batch runs the decode schedule (at most 16 tokens, or chunks of at most 16)
+static bool runs_chunked(const mrun_moe_config &c, int T) {
+    return T > 16 && T <= kChunkedDecodeMax && !is_decode(c, T);
+}
+// the batch runs the decode schedule (whole, or in chunks of at most 16 tokens)
 static bool decode_schedule(const mrun_sparse_moe &m, int T) {
-    if (runs_chunked(T)) return is_decode(m, 16) && is_decode(m, T % 16 ? T % 16 : 16);
+    if (runs_chunked(m.cfg, T)) return is_decode(m, 16) && is_decode(m, T % 16 ? T % 16 : 16);
     return is_decode(m, T);
+}
+// tokens per decode launch of a batch on the decode schedule
+static int decode_launch_tokens(const mrun_moe_config &c, int T) {
+    return runs_chunked(c, T) ? 16 : T;
 }
 static size_t forward_ws_bytes(const mrun_moe_config &c, int T) {
     const size_t plain = make_plan(c, T).total;
-    if (!runs_chunked(T)) return plain;
+    if (!runs_chunked(c, T)) return plain;
     const size_t chunked = chunk_ws_offset(c, T) + make_plan(c, 16).total;
     return plain > chunked ? plain : chunked;
 }
@@ -388,11 +395,12 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
                                  const FusedNorm *fn = nullptr, const PostNorm *post = nullptr,
                                  bool *post_done = nullptr, uint32_t *ids_at = nullptr,
                                  bf16_t *scores_at = nullptr) {
-    // 17 to kChunkedDecodeMax tokens: the decode schedule on chunks of at most 16 tokens (the
-    // tokens of a chunk, then the rest), which streams each chunk's expert rows once, against the
-    // prefill schedule's 64-row tiles that are mostly padding at these sizes. Every token's row
-    // is computed alone as in any decode batch. Instrumented calls (stg) keep one schedule.
-    if (!stg && runs_chunked(T) && decode_schedule(m, T)) {
+    // 17 to kChunkedDecodeMax tokens with more pairs than the decode kernels take (k above 8):
+    // the decode schedule on chunks of at most 16 tokens (the tokens of a chunk, then the rest),
+    // which streams each chunk's expert rows once, against the prefill schedule's 64-row tiles
+    // that are mostly padding at these sizes. Every token's row is computed alone as in any
+    // decode batch. Instrumented calls (stg) keep one schedule.
+    if (!stg && runs_chunked(m.cfg, T) && decode_schedule(m, T)) {
         const mrun_moe_config &c = m.cfg;
         const int D = c.hidden, k = c.top_k;
         if (ws_bytes < forward_ws_bytes(c, T))
@@ -1233,7 +1241,7 @@ int mrun_moe_stack_forward(const mrun_sparse_moe *layers, int32_t n_layers,
         // decode-sized chunks with dense or 4/8-bit routers: the norm runs inside each block's
         // router launch and the residual add inside its last launch (three launches per layer,
         // no norm kernel)
-        const int chunk = tokens < 16 ? tokens : 16;  // tokens per decode launch
+        const int chunk = models::decode_launch_tokens(c, tokens);  // tokens per decode launch
         bool fused = models::decode_schedule(layers[0], tokens) &&
                      2 * (size_t)chunk * D <= 65536;  // the normalised rows fit the router's LDS
         for (int32_t l = 0; fused && l < n_layers; ++l)

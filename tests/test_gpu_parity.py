@@ -252,8 +252,9 @@ def test_block_prefill_4096():
 
 
 def test_rows_keep_their_one_row_bits(q_dev):
-    """A decode batch of T <= 16 rows, and one of up to 32 rows (decode chunks of 16), gives every
-    row the bits of its one-row product (with_row_exact, nuvec.rs:256-265; lanes.rs:68-112)."""
+    """A decode batch of up to 32 rows (256 pairs: T = 24 and 32 fill the third and fourth words
+    of the kernels' pair sets) gives every row the bits of its one-row product (with_row_exact,
+    nuvec.rs:256-265; lanes.rs:68-112)."""
     x_np = synth.make_x(Q, 32, config=synth.CFG_DECODE, layer=77)
     batch = M.bf16_bits(q_dev.forward(M.bf16_tensor(x_np)))
     for T in (8, 16, 17, 24):
@@ -438,8 +439,10 @@ def stack3_gates8():
 @pytest.mark.parametrize("T", [4, 24, 40])
 def test_stack_matches_layer_loop_and_oracle(stack3, T):
     """configs[3]'s decoder-layer loop, x = R(x + MoE_l(rms_norm(x))) per layer, with layer l's
-    residual add and layer l+1's norm fused (add_rms_norm). T=4 takes the decode schedule, T=24 the
-    decode schedule in chunks of 16 and 8 tokens, T=40 the prefill one. Bit-identical to the loop of single ops on the GPU. Against the CPU restatement,
+    residual add and layer l+1's norm fused (add_rms_norm). T=4 takes the decode schedule with the
+    norm inside its router launch, T=24 the decode schedule with the norm as its own launch (24
+    normalised rows exceed the router launch's LDS), T=40 the prefill one. Bit-identical to the
+    loop of single ops on the GPU. Against the CPU restatement,
     layer by layer on the GPU's expert choices (each validated as a top-k within ties): within the
     block bar plus one bf16 ulp of the residual stream (a rounding of x + MoE(h) that lands on the
     neighbouring value moves x by one ulp of |x|, which exceeds 2e-2 where |x| >= 4)."""
@@ -600,9 +603,13 @@ def test_dense_experts_match_oracle(dense_block, T):
 @pytest.mark.parametrize("shape,Ts", [
     # top-1 routing: one pair per token
     (synth.Shape(hidden=2048, experts=64, top_k=1, intermediate=512, shared=512), (1, 16, 100)),
-    # 512 experts (eight per lane in the top-k) with k = 16, the widest top-k; T = 8 is the
-    # decode schedule's limit of 128 pairs, T = 9 the first prefill size
+    # 512 experts (eight per lane in the top-k) with k = 16, the widest top-k (FFN width 256:
+    # the generic GEMV and GEMM at every size)
     (synth.Shape(hidden=2048, experts=512, top_k=16, intermediate=256, shared=0), (1, 8, 9, 70)),
+    # k = 16 on the decode kernels: T = 16 fills their 256 pairs; T = 20 and 32 (more pairs than
+    # that) run as decode chunks of 16 tokens, T = 33 on the prefill schedule
+    (synth.Shape(hidden=2048, experts=128, top_k=16, intermediate=512, shared=512),
+     (16, 20, 32, 33)),
     # k = E: every expert chosen by every token; norm_topk off
     (synth.Shape(hidden=512, experts=8, top_k=8, intermediate=128, shared=128, norm_topk=False),
      (1, 5, 40)),
@@ -615,21 +622,29 @@ def test_config_edges(shape, Ts):
     for T in Ts:
         run_block(hb, dev, synth.make_x(shape, T, config=synth.CFG_PLUMBING, layer=300 + T),
                   f"{shape.name} T={T}")
+    if shape.top_k == 16 and shape.intermediate == 512:
+        # the decode chunks give every row its one-row bits
+        x = synth.make_x(shape, 20, config=synth.CFG_PLUMBING, layer=320)
+        batch = M.bf16_bits(dev.forward(M.bf16_tensor(x)))
+        for t in (0, 15, 16, 19):
+            one = M.bf16_bits(dev.forward(M.bf16_tensor(x[t:t + 1])))
+            assert np.array_equal(one[0], batch[t]), f"chunked row {t}"
+
 
 
 def test_decode_boundary_t33(q_host, q_dev):
-    """T = 32 is the last size that runs as decode chunks and T = 33 the first prefill one: the same
-    token's output agrees between them within the bar (the two schedules accumulate in different
-    orders), and T = 17 (a chunk of 16, then one of 1) gives its rows the T = 16 bits."""
+    """T = 32 is the last size that runs the decode kernels and T = 33 the first prefill one: the
+    same token's output agrees between them within the bar (the two schedules accumulate in
+    different orders), and T = 17 gives its rows the T = 16 bits."""
     x33 = synth.make_x(Q, 33, config=synth.CFG_DECODE, layer=17)
     a = M.bf16_bits(q_dev.forward(M.bf16_tensor(x33)))
     b = M.bf16_bits(q_dev.forward(M.bf16_tensor(x33[:32])))
     c = M.bf16_bits(q_dev.forward(M.bf16_tensor(x33[:17])))
     d = M.bf16_bits(q_dev.forward(M.bf16_tensor(x33[:16])))
     torch.cuda.synchronize()
-    assert_close(b, a[:32], what="T=32 decode chunks vs T=33 prefill rows")
+    assert_close(b, a[:32], what="T=32 decode vs T=33 prefill rows")
     assert np.array_equal(c[:16], d), "T=17 rows 0-15 against T=16"
-    assert_close(c, a[:17], what="T=17 decode chunks vs T=33 prefill rows")
+    assert_close(c, a[:17], what="T=17 decode vs T=33 prefill rows")
 
 
 # ---------------------------------------------------------------------------------------------

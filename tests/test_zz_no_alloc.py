@@ -33,7 +33,7 @@ def test_noalloc_matches_forward(shape, Ts):
     hb = synth.make_block(shape, config=synth.CFG_DECODE, layer=900)
     dev = M.SparseMoe(hb)
     cap = int(_lib.load().mrun_moe_forward_noalloc_max_bytes())
-    for T in Ts:  # prefill first, then smaller decode batches (24: two chunks) over stale scratch
+    for T in Ts:  # prefill first, then smaller decode batches over stale scratch contents
         assert dev.workspace_bytes(T) <= cap
         x = M.bf16_tensor(synth.make_x(shape, T, config=synth.CFG_DECODE, layer=900 + T))
         want = M.bf16_bits(dev.forward(x))
