@@ -321,7 +321,7 @@ def calib_lib():
     return lib
 
 
-def launch_floor(torch, grids=(65, 576, 256), reps: int = 200) -> dict:
+def launch_floor(torch, grids=(65, 288, 256), reps: int = 200) -> dict:
     """The floor under the decode forward's three dependent launches: chains of three launches
     with the T = 1 forward's grids (router, gate/up, down), each workgroup storing a word for the
     next launch, timed like the forward (HIP events around `reps` back-to-back chains). `read`:
