@@ -119,7 +119,7 @@ struct GemvJob {
 hipError_t launch_gemv(const GemvJob &job, hipStream_t stream);
 
 // The decode schedule (decode.hip): router + shared expert gate/up, routed gate/up, down +
-// combine, for T <= 16 tokens and T*k <= 128 pairs.
+// combine, for T <= 32 tokens and T*k <= 256 pairs.
 struct DecodeJob {
     const bf16_t *x;
     int T, D, E, k, I, S, norm, max_slots;
@@ -210,6 +210,7 @@ struct MoeGemmJob {
     QW w0, w1;
     Routing routing;
     int has_routing, max_tiles;
+    int tile_m;  // rows per tile: 64, or 32 (the routed tiles cut to 32 rows by the permute)
     int M;
     bf16_t *out;
     int ldo;

@@ -192,7 +192,8 @@ static Plan make_plan(const mrun_moe_config &c, int T) {
     };
     const size_t E = c.experts, D = c.hidden, I = c.intermediate, S = c.shared_intermediate;
     const size_t P = (size_t)T * c.top_k;
-    p.max_tiles = (int)((P + kGemmTileM - 1) / kGemmTileM + E);
+    // tiles of 64 rows, or of 32 (mid-size batches on the grouped GEMM): room for the smaller
+    p.max_tiles = (int)((P + 31) / 32 + E);
     p.logits = take(2 * (size_t)T * E);
     p.ids = take(4 * P);
     p.scores = take(2 * P);
@@ -360,6 +361,12 @@ struct FusedNorm {
 // post (the layer stack): when the forward ends in the combine launch and its rows are at most
 // 2048 wide, that launch also takes the stack's residual add and next RMSNorm (post_done set, and
 // `out` is not written).
+// Prefill batches whose experts average at most this many rows have their routed tiles cut to 32
+// rows for the grouped GEMM. On the configs[1] block (per block, 32- against 64-row tiles):
+// T = 33 131 -> 111 us, 64 154 -> 132, 128 164 -> 144, 256 180 -> 159, 512 190 -> 165, 768 199 ->
+// 179; T = 1024 (32 rows on average) the same; T = 2048 281 -> 308 (Zipf router: 268 -> 311).
+constexpr int kHalfTileMaxRows = 28;
+
 // the largest batch that runs as decode-schedule chunks of at most 16 tokens, when the decode
 // kernels do not take it whole (more than 256 pairs: k above 8)
 constexpr int kChunkedDecodeMax = 32;
@@ -521,14 +528,6 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
     TRY_HIP(launch_topk_count(logits, T, E, k, c.norm_topk_prob != 0, ids, scores, counts, s),
             "top-k");
     st.mark(s);
-    PermuteOut pt = po;
-    pt.tiles = (uint32_t *)at(p.tiles);
-    pt.n_tiles = (uint32_t *)at(p.n_tiles);
-    if (packs) pt.tile_rows = (uint32_t *)at(p.tile_rows);
-    TRY_HIP(launch_route_scatter(ids, counts, T, k, E, pt, s), "scatter");
-    if (packs && !packed)
-        TRY_HIP(launch_apack(x, D, T, D, (bf16_t *)at(p.xp), D, (bf16_t *)at(p.xs), s), "pack x");
-    st.mark(s);
     // the grouped GEMM of moe_gemm.hip: 4-bit group-64 experts, K a multiple of 512, the shared
     // expert in the same launches when its width equals the routed one
     MoeGemmJob mg{}, md{};
@@ -556,6 +555,19 @@ static Status sparse_moe_forward(const mrun_sparse_moe &m, const bf16_t *x, int 
             if (moe_gemm_supported(tg) && moe_gemm_supported(td)) mg = tg, md = td, fuse_new = true;
         }
     }
+    // mid-size batches: the routed tiles cut to 32 rows (most experts hold a few rows, so a 64-row
+    // tile is mostly padding), on the grouped GEMM's one-row-fragment instantiation
+    const bool half = new_path && (long long)P <= (long long)kHalfTileMaxRows * E;
+    mg.tile_m = md.tile_m = half ? 32 : kGemmTileM;
+    PermuteOut pt = po;
+    pt.tile_m = half ? 32 : kGemmTileM;
+    pt.tiles = (uint32_t *)at(p.tiles);
+    pt.n_tiles = (uint32_t *)at(p.n_tiles);
+    if (packs) pt.tile_rows = (uint32_t *)at(p.tile_rows);
+    TRY_HIP(launch_route_scatter(ids, counts, T, k, E, pt, s), "scatter");
+    if (packs && !packed)
+        TRY_HIP(launch_apack(x, D, T, D, (bf16_t *)at(p.xp), D, (bf16_t *)at(p.xs), s), "pack x");
+    st.mark(s);
     if (new_path) {
         TRY_HIP(launch_moe_gemm(mg, s), "gate/up (moe gemm)");
         st.mark(s);

@@ -174,7 +174,10 @@ __device__ __forceinline__ int xrow_of(int l) {
     return 32 * (fr >> 4) + 8 * ((fr >> 2) & 3) + 4 * (l >> 5) + (fr & 3);
 }
 
-template <bool GLU>
+// HALF: tiles of at most 32 rows (the batch's routed tiles cut to 32 rows, the shared expert's
+// rows in tiles of 32): the second row fragment's MFMAs, scale FMAs, bias term and epilogue are
+// left out. The copies still fill 64 A rows (rows past a tile's own repeat its last one).
+template <bool GLU, bool HALF = false>
 __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
     using namespace mg;
     __shared__ __align__(16) char smem[LDS_BYTES];
@@ -185,9 +188,11 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
 
     constexpr int NCOLS = GLU ? 128 : 256;
     const int NB = j.N / NCOLS;
-    const int s_tiles = j.has_shared ? (j.sh.M + BM - 1) / BM : 0;
+    constexpr int TM = HALF ? 32 : BM;  // rows per tile
+    constexpr int NMI = HALF ? 1 : 2;   // row fragments of 32 rows
+    const int s_tiles = j.has_shared ? (j.sh.M + TM - 1) / TM : 0;
     const int r_tiles =
-        j.has_routing ? min((int)*j.routing.n_tiles, j.max_tiles) : (j.M + BM - 1) / BM;
+        j.has_routing ? min((int)*j.routing.n_tiles, j.max_tiles) : (j.M + TM - 1) / TM;
     const int total = (s_tiles + r_tiles) * NB;
     const int G8 = (int)(gridDim.x >> 3), xcd = (int)(blockIdx.x & 7), slot = (int)(blockIdx.x >> 3);
     const int seg_lo = (int)((long long)total * xcd / 8);
@@ -216,7 +221,7 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
         Item it;
         it.n0 = cb * NCOLS;
         if (rt < s_tiles) {
-            it.sh = true, it.e = 0, it.row0 = rt * BM, it.mrows = min(BM, j.sh.M - it.row0);
+            it.sh = true, it.e = 0, it.row0 = rt * TM, it.mrows = min(TM, j.sh.M - it.row0);
             it.tile = -1;
         } else {
             it.sh = false;
@@ -228,7 +233,7 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
                 it.e = uni((int)e), it.row0 = uni((int)row0), it.mrows = uni((int)mrows);
                 it.tile = j.tile_rows ? r : -1;
             } else {
-                it.e = 0, it.row0 = r * BM, it.mrows = min(BM, j.M - it.row0), it.tile = -1;
+                it.e = 0, it.row0 = r * TM, it.mrows = min(TM, j.M - it.row0), it.tile = -1;
             }
         }
         return it;
@@ -272,9 +277,10 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
         const int r = rt - s_tiles;
         dma4(rsrc_of(j.routing.tiles, 12u * (uint32_t)j.max_tiles), 4u * (uint32_t)lane,
              12u * (uint32_t)r, smem + OFF_T + (n & 1) * T_BYTES);
+        // 64 entries from tile r's first (those past the table read as 0: its resource's size)
         if (j.tile_rows)
-            dma4(rsrc_of(j.tile_rows), 4u * (uint32_t)lane, 4u * (uint32_t)(r * BM),
-                 rowbuf + (n & 1) * R_BYTES);
+            dma4(rsrc_of(j.tile_rows, 4u * (uint32_t)j.max_tiles * (uint32_t)TM),
+                 4u * (uint32_t)lane, 4u * (uint32_t)(r * TM), rowbuf + (n & 1) * R_BYTES);
     };
     auto setup_load = [&](int n) __attribute__((always_inline)) {
         const Item it = item_of(n);
@@ -501,9 +507,10 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
                                 : (s == 0 ? a00 : s == 1 ? a01 : s == 2 ? a02 : a03);
             mg_f32x16 &pt = ni ? part1[mi] : part0[mi];
             const mg_f32x16 z = {};
-            pt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(mg_bf16x8, af),
-                                                        __builtin_bit_cast(mg_bf16x8, e),
-                                                        s ? pt : z, 0, 0, 0);
+            if (!(HALF && mi))  // (HALF: no second row fragment; its A reads keep the wait counts)
+                pt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(mg_bf16x8, af),
+                                                            __builtin_bit_cast(mg_bf16x8, e),
+                                                            s ? pt : z, 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             if (SS && (q & 1)) issue_part(q >> 1, SLOT_N);
             // 4 scale FMAs: slot q's share of pend (q < 8) or of fragment 0 (q >= 8)
@@ -514,6 +521,7 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
 #pragma unroll
             for (int i = 4 * (q & 3); i < 4 * (q & 3) + 4; ++i) {
                 const int fm = (q & 7) >> 2;
+                if (HALF && fm) continue;
                 if (q < 8) acc[fm][1][i] += sc_pend * part1[fm][i];
                 else acc[fm][0][i] += sc0 * part0[fm][i];
             }
@@ -555,7 +563,7 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
                     v = u32x4{0u, 0u, 0u, 0u};
                 }
 #pragma unroll
-                for (int mi = 0; mi < 2; ++mi)
+                for (int mi = 0; mi < NMI; ++mi)
 #pragma unroll
                     for (int tt = 0; tt < 3; ++tt)
                         acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
@@ -566,7 +574,7 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
         if (ST != 3 || ks != nks - 1) return;
         // the item's last fragment-1 scale
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
+        for (int mi = 0; mi < NMI; ++mi)
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[mi][1][i] += sc_pend * part1[mi][i];
         sc_pend = 0.f;
@@ -589,8 +597,11 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
             const int pcol = (col & ~63) + 8 * (2 * (kb & 3) + (kb >> 2)) + 2 * (jj & 3);
             const bool hi4 = (jj & 4) != 0;
             float va[2][16];  // the act values (rounded) of rows mi * 32 + 8 (i / 4) + 4 fh + i % 4
+            if (HALF)
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
+                for (int i = 0; i < 16; ++i) va[1][i] = 0.f;
+#pragma unroll
+            for (int mi = 0; mi < NMI; ++mi)
 #pragma unroll
                 for (int i = 0; i < 16; i += 2) {
                     float v[2];
@@ -669,7 +680,7 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
             for (int ni = 0; ni < 2; ++ni) {
                 const int col8 = ci.n0 + (ni ? bro1 : bro0) + (fr & ~7);
 #pragma unroll
-                for (int mi = 0; mi < 2; ++mi) {
+                for (int mi = 0; mi < NMI; ++mi) {
                     uint2 w4[4];
 #pragma unroll
                     for (int b = 0; b < 4; ++b) {
@@ -740,6 +751,7 @@ bool moe_gemm_supported(const MoeGemmJob &j) {
     };
     const int ncols = j.glu ? 128 : 256;
     if (j.N <= 0 || j.N % ncols != 0 || !ok(j.w0, j.K) || (j.glu && !ok(j.w1, j.K))) return false;
+    if (j.tile_m != 0 && j.tile_m != 32 && j.tile_m != 64) return false;  // rows per tile
     // A row offsets (row * lda * 2 bytes, through a buffer resource) are 32-bit
     auto a_fits = [](long long rows, int lda) { return rows > 0 && rows * lda * 2 < (1LL << 32); };
     if (!a_fits(j.a_rows, j.lda) || (j.has_shared && !a_fits(j.sh.M, j.sh.lda))) return false;
@@ -785,15 +797,22 @@ hipError_t launch_moe_gemm(const MoeGemmJob &j, hipStream_t stream) {
     if (!moe_gemm_supported(j)) return hipErrorInvalidValue;
     const int ncols = j.glu ? 128 : 256;
     const int nb = j.N / ncols;
-    const int s_tiles = j.has_shared ? (j.sh.M + mg::BM - 1) / mg::BM : 0;
-    const int r_tiles = j.has_routing ? j.max_tiles : (j.M + mg::BM - 1) / mg::BM;
+    const int tm = j.tile_m == 32 ? 32 : mg::BM;
+    const int s_tiles = j.has_shared ? (j.sh.M + tm - 1) / tm : 0;
+    const int r_tiles = j.has_routing ? j.max_tiles : (j.M + tm - 1) / tm;
     const long long items = (long long)(s_tiles + r_tiles) * nb;
     if (items == 0) return hipSuccess;
     long long grid = 2LL * cu_count();
     if (grid > items) grid = items;
     grid = (grid + 7) / 8 * 8;
-    if (j.glu) moe_gemm_kernel<true><<<(unsigned)grid, mg::NT, 0, stream>>>(j);
-    else moe_gemm_kernel<false><<<(unsigned)grid, mg::NT, 0, stream>>>(j);
+    if (tm == 32) {
+        if (j.glu) moe_gemm_kernel<true, true><<<(unsigned)grid, mg::NT, 0, stream>>>(j);
+        else moe_gemm_kernel<false, true><<<(unsigned)grid, mg::NT, 0, stream>>>(j);
+    } else if (j.glu) {
+        moe_gemm_kernel<true><<<(unsigned)grid, mg::NT, 0, stream>>>(j);
+    } else {
+        moe_gemm_kernel<false><<<(unsigned)grid, mg::NT, 0, stream>>>(j);
+    }
     return hipGetLastError();
 }
 

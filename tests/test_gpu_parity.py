@@ -331,8 +331,10 @@ def test_block_coder_decode(T):
             assert np.array_equal(one[0], batch[t]), f"row {t}"
 
 
-def test_block_coder_prefill_rows():
-    T = 1024
+@pytest.mark.parametrize("T", [300, 1024])
+def test_block_coder_prefill_rows(T):
+    """configs[4] at prefill sizes: T = 300 (15 rows per expert on average) on the grouped GEMM's
+    32-row tiles, T = 1024 on its 64-row tiles."""
     hb = _coder_host()
     dev = _coder_dev()
     x_np = synth.make_x(synth.CODER, T, config=synth.CFG_CODER, layer=T)
@@ -341,6 +343,17 @@ def test_block_coder_prefill_rows():
 
 
 WIDE_SHARED = synth.Shape(hidden=4096, experts=64, top_k=8, intermediate=1024, shared=1024)
+
+
+def test_wide_rows_with_shared_expert_prefill():
+    """The same block at T = 40 (five rows per expert on average): the grouped GEMM's 32-row tiles,
+    with the shared expert's rows as tiles of 32 in the same launches. Against the oracle."""
+    if "wide" not in _CODER:
+        hb = synth.make_block(WIDE_SHARED, config=synth.CFG_DECODE, layer=7)
+        _CODER["wide"] = (hb, M.SparseMoe(hb))
+    hb, dev = _CODER["wide"]
+    run_block(hb, dev, synth.make_x(WIDE_SHARED, 40, config=synth.CFG_DECODE, layer=340),
+              "wide rows with a shared expert, prefill T=40")
 
 
 @pytest.mark.parametrize("T", [1, 2, 5])

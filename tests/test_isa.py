@@ -46,7 +46,7 @@ def _kernel_bodies(asm):
         start = asm.index(f"\n{name}:") + 1
         end = asm.index("s_endpgm", start)
         bodies[name] = asm[start:end].splitlines()
-    assert len(bodies) == 2, "both moe_gemm_kernel instantiations"
+    assert len(bodies) == 4, "the moe_gemm_kernel instantiations (gate/up, down; 64- and 32-row tiles)"
     return bodies
 
 
