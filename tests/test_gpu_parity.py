@@ -265,6 +265,19 @@ def test_rows_keep_their_one_row_bits(q_dev):
         assert np.array_equal(one[0], batch[t]), f"row {t}"
 
 
+def test_prefill_rows_keep_their_bits(q_dev):
+    """On the prefill schedule (T >= 33) a token's output has the same bits whatever batch it is in
+    and whichever tile class the grouped GEMM runs: T = 897 (7,176 pairs, 64-row tiles) against its
+    first 896 rows (7,168 = 28 E pairs, the last size on 32-row tiles), 300 and 33 rows. Every row's
+    sums run in one order (K steps in sequence, the bias term per 8 of them), whatever tile holds
+    the row."""
+    x_np = synth.make_x(Q, 897, config=synth.CFG_DECODE, layer=897)
+    full = M.bf16_bits(q_dev.forward(M.bf16_tensor(x_np)))
+    for T in (896, 300, 33):
+        b = M.bf16_bits(q_dev.forward(M.bf16_tensor(x_np[:T])))
+        assert np.array_equal(b, full[:T]), f"T={T}"
+
+
 def test_empty_batch(q_dev):
     """T = 0: the block, the router and the stack return empty results and enqueue nothing."""
     x = torch.empty(0, Q.hidden, dtype=torch.bfloat16, device="cuda")
