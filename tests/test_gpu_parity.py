@@ -529,11 +529,12 @@ def q8_blocks():
 
 
 @pytest.mark.parametrize("kind", ["experts8", "gates8", "both8"])
-@pytest.mark.parametrize("T", [1, 3, 16, 40, 300])
+@pytest.mark.parametrize("T", [1, 3, 16, 24, 40, 300])
 def test_8bit_weights_match_oracle(q8_blocks, kind, T):
-    """8-bit experts run the decode kernels at T <= 16 (each byte's two nibbles dotted as two 4-bit
-    codes) and the generic MFMA GEMM above; an 8-bit router and shared gate are dequantized inside
-    the decode router launch (T <= 16) or run as the prefill's first product."""
+    """8-bit experts run the decode kernels at T <= 32 (each byte's two nibbles dotted as two 4-bit
+    codes; T = 24 as one batch of 192 pairs) and the generic MFMA GEMM above; an 8-bit router and
+    shared gate are dequantized inside the decode router launch (T <= 32) or run as the prefill's
+    first product."""
     hb, dev = q8_blocks[kind]
     x_np = synth.make_x(Q8, T, config=synth.CFG_DECODE, layer=100 + T)
     run_block(hb, dev, x_np, f"{kind} T={T}")
