@@ -328,11 +328,12 @@ def test_forward_is_deterministic(q_dev):
     assert np.array_equal(a, b)
 
 
-@pytest.mark.parametrize("T", [1, 3, 8, 16])
+@pytest.mark.parametrize("T", [1, 3, 8, 16, 24])
 def test_block_coder_decode(T):
     """configs[4] at decode: hidden 6144, 160 experts, FFN 2560, no shared expert (the streaming
-    gate/up and down kernels; T = 3 leaves waves of the down kernel with fewer pairs than others).
-    Against the oracle, and every row equal to its one-row forward."""
+    gate/up and down kernels; T = 3 leaves waves of the down kernel with fewer pairs than others;
+    T = 24 is one decode batch of 192 pairs). Against the oracle, and every row equal to its
+    one-row forward."""
     hb = _coder_host()
     dev = _coder_dev()
     x_np = synth.make_x(synth.CODER, T, config=synth.CFG_CODER, layer=T)
@@ -369,7 +370,7 @@ def test_wide_rows_with_shared_expert_prefill():
               "wide rows with a shared expert, prefill T=40")
 
 
-@pytest.mark.parametrize("T", [1, 2, 5])
+@pytest.mark.parametrize("T", [1, 2, 5, 24])
 def test_wide_rows_with_shared_expert(T):
     """Rows wider than 2048 with a shared expert: the decode gate/up streams two row blocks per
     workgroup (routed and shared workgroups; one pair at T = 1, two pairs at a time above), the
