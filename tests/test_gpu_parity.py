@@ -641,6 +641,10 @@ def test_dense_experts_match_oracle(dense_block, T):
     # k = E: every expert chosen by every token; norm_topk off
     (synth.Shape(hidden=512, experts=8, top_k=8, intermediate=128, shared=128, norm_topk=False),
      (1, 5, 40)),
+    # norm_topk off on the tuned kernels (the Qwen3.6-like shape): the top-k inside the decode
+    # gate/up launch (T <= 4), the top-k launch (T = 24), the prefill top-k + counts (T = 300)
+    (synth.Shape(hidden=2048, experts=256, top_k=8, intermediate=512, shared=512,
+                 norm_topk=False), (1, 4, 24, 300)),
     # hidden not a multiple of 64 (the MFMA paths need K % 64 == 0; group 32): GEMV at every size
     (synth.Shape(hidden=2080, experts=32, top_k=4, intermediate=544, shared=0, group=32), (2, 33)),
 ])
