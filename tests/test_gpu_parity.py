@@ -241,6 +241,22 @@ def test_block_prefill_zipf_2048():
     _log(f"zipf: hottest expert {counts.max()} pairs = {counts.max() / counts.mean():.1f}x mean")
 
 
+@pytest.fixture(scope="module")
+def zipf_block():
+    hb = synth.make_block(Q, config=synth.CFG_PREFILL_ZIPF, zipf=True)
+    return hb, M.SparseMoe(hb)
+
+
+@pytest.mark.parametrize("T", [1, 4, 24, 300])
+def test_block_router_bias(zipf_block, T):
+    """The configs[2] block (a router bias from the Zipf ranking, so hot experts take many of a
+    batch's pairs) at decode sizes, where the router launch adds the bias (T = 24: one decode batch,
+    the hottest experts with several pairs each), and at T = 300 on 32-row tiles."""
+    hb, dev = zipf_block
+    run_block(hb, dev, synth.make_x(Q, T, config=synth.CFG_PREFILL_ZIPF, layer=500 + T),
+              f"router bias T={T}")
+
+
 def test_block_prefill_4096():
     """configs[3]'s prefill chunk, T = 4096 (experts average 128 rows; the shared expert rides in the
     expert launches)."""
