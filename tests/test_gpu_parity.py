@@ -580,6 +580,20 @@ def test_8bit_groups(group):
                   f"8-bit group {group} T={T}")
 
 
+@pytest.mark.parametrize("group", [32, 128])
+def test_groups_on_the_decode_kernels(group):
+    """4-bit experts with groups of 32 and 128 on the Qwen3.6-like shape: the decode kernels (a
+    lane's 32-code chunk lies in one group, its scale and bias picked by the group shift) at
+    T = 1, 4 and 24, and the generic MFMA GEMM at T = 300."""
+    shape = synth.Shape(hidden=2048, experts=256, top_k=8, intermediate=512, shared=512,
+                        group=group)
+    hb = synth.make_block(shape, config=synth.CFG_DECODE, layer=group)
+    dev = M.SparseMoe(hb)
+    for T in (1, 4, 24, 300):
+        run_block(hb, dev, synth.make_x(shape, T, config=synth.CFG_DECODE, layer=600 + T),
+                  f"4-bit group {group} T={T}")
+
+
 def test_quantized_linear_facade():
     """Linear::forward with an 8-bit weight and a bias (load.rs:294-306): R(R(x Wq^T) + b)."""
     w = synth.normal_bf16(synth.seed(9, 0, synth.ROUTER_W), 96 * 512, 0.02).reshape(96, 512)
