@@ -210,6 +210,19 @@ def test_workspace_contract():
     assert rc == _lib.MRUN_ERR_INVALID
 
 
+def test_every_decode_batch_fits_the_noalloc_scratch():
+    """mrun_moe_forward_noalloc takes every decode batch (T <= 32): the workspace of the widest
+    configuration the decode kernels accept (hidden, FFN and shared widths 8192, 512 experts,
+    k = 16, 32 tokens) fits its scratch array, and so does a Qwen3.6-like prefill chunk of 512."""
+    lib = _lib.load()
+    lim = lib.mrun_moe_forward_noalloc_max_bytes()
+    assert lim == 32 << 20
+    for cfg, T in ((MoeConfig(8192, 512, 16, 8192, 1, 8192), 32),
+                   (MoeConfig(6144, 160, 8, 2560, 1, 0), 32),
+                   (MoeConfig(2048, 256, 8, 512, 1, 512), 512)):
+        assert 0 < lib.mrun_moe_workspace_bytes(ctypes.byref(cfg), T) <= lim, (cfg.hidden, T)
+
+
 def test_op_argument_errors():
     lib = _lib.load()
     rc = lib.mrun_moe_permute(FAKE, 10, 3, 16, FAKE, None, None, None, None, 0, None)
