@@ -120,7 +120,7 @@ int mrun_moe_forward_f32(const mrun_sparse_moe *moe, const float *x, int32_t tok
  * tight serving loops, harnesses that forbid hipMalloc). It has no counterpart in the reference.
  * The workspace is a fixed scratch array inside the library, one per GPU, held until the process
  * ends: mrun_moe_forward_noalloc_max_bytes() bytes (32 MiB: every decode batch, and prefill
- * chunks whose mrun_moe_workspace_bytes fits, e.g. a few hundred tokens of the Qwen3.6-like
+ * chunks whose mrun_moe_workspace_bytes fits, e.g. up to 649 tokens of the Qwen3.6-like
  * block). A batch that needs more returns MRUN_ERR_WORKSPACE. The call allocates nothing; the
  * caller still passes x and out. Every call on one GPU shares that GPU's array, so calls that
  * overlap in time on one GPU (two streams, two threads) race: serialise them.
