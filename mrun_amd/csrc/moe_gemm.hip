@@ -176,7 +176,8 @@ __device__ __forceinline__ int xrow_of(int l) {
 
 // HALF: tiles of at most 32 rows (the batch's routed tiles cut to 32 rows, the shared expert's
 // rows in tiles of 32): the second row fragment's MFMAs, scale FMAs, bias term and epilogue are
-// left out. The copies still fill 64 A rows (rows past a tile's own repeat its last one).
+// left out, and so are the copies of A rows 32-63 (their LDS fragment reads stay, unused, so
+// every LDS wait count is the same in both instantiations).
 template <bool GLU, bool HALF = false>
 __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
     using namespace mg;
@@ -312,6 +313,7 @@ __global__ __launch_bounds__(mg::NT, 2) void moe_gemm_kernel(MoeGemmJob j) {
         constexpr int SLOT = decltype(slot_c)::value;
         char *sa = smem + SLOT * STAGE, *sc = sa + A_BYTES;
         if (part < 4) {
+            if (HALF && (part & 1)) return;  // A rows 32-63: no MFMA of a 32-row tile reads them
             const int kk = part >> 1;
             dma16(r_a, (part & 1) ? la1 : la0, 128u * (l_ks + kk),
                   sa + kk * A_STEP + (part & 1) * 4096 + wave * 1024);
